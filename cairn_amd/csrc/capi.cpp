@@ -1,0 +1,317 @@
+// The C ABI of libcairn_gemm_gfx950.so (include/cairn_gemm.h): the kernel table, the checks a descriptor must pass,
+// the tile selector and the launch. No allocation, no stream or event made, no wait: cairn_gemm_run only queues.
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include "../../include/cairn_gemm.h"
+#include "kernels.hpp"
+
+using cairn::gemm::Params;
+using Launcher = hipError_t (*)(const Params&, hipStream_t);
+
+#define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
+#include "instances.inc"
+#undef CAIRN_MFMA_INSTANCE
+hipError_t cairn_generic(const Params&, hipStream_t);
+hipError_t cairn_skinny(const Params&, hipStream_t, int split);
+
+namespace {
+
+constexpr int CUS = 256;              // gfx950: 8 XCDs of 32 CUs (MI350X, MI355X)
+constexpr int LDS_PER_CU = 160 * 1024;
+
+enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2 };
+
+struct Kernel {
+  Launcher run;
+  int family;
+  int op;  // cairn::gemm::OP_*; the generic and skinny kernels take every type they are given
+  bool ta, tb;
+  int bm, bn;
+  const char* name;
+};
+
+#define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) {NAME, MFMA, OP, TA, TB, BM, BN, #NAME},
+const Kernel TABLE[] = {
+    {nullptr, GENERIC, -1, false, false, 64, 64, "cairn_generic_64x64"},
+    {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 32, "cairn_skinny_bf16_nt"},
+#include "instances.inc"
+};
+#undef CAIRN_MFMA_INSTANCE
+constexpr int COUNT = int(sizeof(TABLE) / sizeof(TABLE[0]));
+
+int op_of(int type) {
+  switch(type) {
+    case CAIRN_TYPE_BF16: return cairn::gemm::OP_BF16;
+    case CAIRN_TYPE_F16: return cairn::gemm::OP_F16;
+    case CAIRN_TYPE_I8: return cairn::gemm::OP_I8;
+    default: return -1;  // the 8-bit floats: the generic kernel widens them
+  }
+}
+int element_size(int type) { return type == CAIRN_TYPE_BF16 || type == CAIRN_TYPE_F16 ? 2 : 1; }
+int output_size(int type) { return type == CAIRN_TYPE_F32 || type == CAIRN_TYPE_I32 ? 4 : 2; }
+bool aligned(const void* p, std::uint64_t bytes) { return reinterpret_cast<std::uintptr_t>(p) % bytes == 0; }
+
+// A descriptor with its leading dimensions filled in, checked.
+struct Problem {
+  cairn_gemm_desc d;
+  bool empty;  // nothing to queue
+};
+
+int check(const cairn_gemm_desc* in, Problem& out) {
+  if(!in || in->version != CAIRN_GEMM_DESC_VERSION) return CAIRN_E_ARG;
+  cairn_gemm_desc d = *in;
+  const int t = d.ab_type;
+  if(t != CAIRN_TYPE_F16 && t != CAIRN_TYPE_BF16 && t != CAIRN_TYPE_F8E4M3 && t != CAIRN_TYPE_F8E5M2 &&
+     t != CAIRN_TYPE_I8)
+    return CAIRN_E_TYPE;
+  const bool epilogue = d.bias || d.row_scale || d.col_scale || d.act != CAIRN_ACT_NONE;
+  if(d.c_type == CAIRN_TYPE_I32) {
+    if(t != CAIRN_TYPE_I8 || epilogue || d.accumulate) return CAIRN_E_TYPE;  // the accumulator itself
+  } else if(d.c_type != CAIRN_TYPE_F32 && d.c_type != CAIRN_TYPE_BF16 && d.c_type != CAIRN_TYPE_F16) {
+    return CAIRN_E_TYPE;
+  }
+  if(d.accumulate && d.c_type != CAIRN_TYPE_F32) return CAIRN_E_TYPE;
+  if(d.act < CAIRN_ACT_NONE || d.act > CAIRN_ACT_GELU) return CAIRN_E_ARG;
+  if(d.bias && d.bias_type != CAIRN_TYPE_F32 && d.bias_type != CAIRN_TYPE_BF16) return CAIRN_E_TYPE;
+  if((d.trans_a != 0 && d.trans_a != 1) || (d.trans_b != 0 && d.trans_b != 1)) return CAIRN_E_ARG;
+  constexpr std::uint64_t LIMIT = 0x7fffffffULL;
+  if(d.m > LIMIT || d.n > LIMIT || d.k > LIMIT) return CAIRN_E_SHAPE;
+  const std::uint64_t arow = d.trans_a ? d.m : d.k, brow = d.trans_b ? d.k : d.n;
+  if(!d.lda) d.lda = arow;
+  if(!d.ldb) d.ldb = brow;
+  if(!d.ldc) d.ldc = d.n;
+  if(d.lda < arow || d.ldb < brow || d.ldc < d.n) return CAIRN_E_SHAPE;
+  out.empty = d.m == 0 || d.n == 0 || (d.k == 0 && d.c_type == CAIRN_TYPE_F32 && d.accumulate && !epilogue);
+  if(!out.empty) {
+    if(!d.c) return CAIRN_E_ARG;
+    if(d.k && (!d.a || !d.b)) return CAIRN_E_ARG;
+    // Workgroup counts and element offsets fit the kernels' int32 and 64-bit arithmetic.
+    if(((d.m + 63) / 64) * ((d.n + 63) / 64) > LIMIT) return CAIRN_E_SHAPE;
+  }
+  out.d = d;
+  return CAIRN_OK;
+}
+
+// Can the tiled MFMA kernel take this problem: its 16-byte chunks whole and aligned, its offsets inside int32.
+bool mfma_fits(const cairn_gemm_desc& d, const Kernel& k) {
+  if(k.family != MFMA || k.op != op_of(d.ab_type) || k.ta != bool(d.trans_a) || k.tb != bool(d.trans_b)) return false;
+  const int es = element_size(d.ab_type), ce = 16 / es;
+  const std::uint64_t bk = 128 / es;
+  auto kmajor = [&](const void* p, std::uint64_t ld, int rows) {
+    return d.k % ce == 0 && ld % ce == 0 && aligned(p, 16) && std::uint64_t(rows) * ld * es < 0x7fff0000ULL;
+  };
+  auto mnmajor = [&](const void* p, std::uint64_t ld, std::uint64_t cols) {
+    return cols % 8 == 0 && ld % 8 == 0 && aligned(p, 8 * es) && bk * ld * es < 0x7fff0000ULL;
+  };
+  const bool a_ok = d.trans_a ? mnmajor(d.a, d.lda, d.m) : kmajor(d.a, d.lda, k.bm);
+  const bool b_ok = d.trans_b ? kmajor(d.b, d.ldb, k.bn) : mnmajor(d.b, d.ldb, d.n);
+  const int os = output_size(d.c_type);
+  const bool c_ok = d.n % 4 == 0 && d.ldc % 4 == 0 && aligned(d.c, 4 * os);
+  return a_ok && b_ok && c_ok;
+}
+
+// The skinny kernel: bf16, b stored n x k (the decode layout), m <= 16, every row 16-byte whole.
+bool skinny_fits(const cairn_gemm_desc& d) {
+  return d.ab_type == CAIRN_TYPE_BF16 && !d.trans_a && d.trans_b && d.m <= 16 && d.k % 8 == 0 && d.lda % 8 == 0 &&
+         d.ldb % 8 == 0 && aligned(d.a, 16) && aligned(d.b, 16) && d.lda * 2 * 16 < 0x7fff0000ULL &&
+         d.ldb * 2 * 64 < 0x7fff0000ULL;
+}
+
+// Workgroups of a tile shape one CU holds at once: LDS is the limit (two stages of both operands).
+int resident(const Kernel& k) {
+  if(k.family != MFMA) return 8;
+  const int lds = 2 * (k.bm + k.bn) * 128;
+  return std::max(1, std::min(2, LDS_PER_CU / lds));
+}
+
+// The share of the MFMA rate a tile shape sustains, relative to 256 x 256: smaller tiles read more operand bytes per
+// MFMA from LDS and L2. These are the selector's model, refit from the measured rates the benchmark records.
+double shape_rate(const Kernel& k) {
+  const int area = k.bm * k.bn;
+  if(area >= 256 * 256) return 1.0;
+  if(area >= 256 * 128) return 0.92;
+  return 0.78;
+}
+
+struct Estimate {
+  double cost, waves, efficiency;
+  std::uint64_t workgroups;
+};
+
+Estimate estimate(const cairn_gemm_desc& d, const Kernel& k) {
+  Estimate e{};
+  if(k.family == SKINNY) {
+    const std::uint64_t blocks = (d.n + k.bn - 1) / k.bn;
+    e.workgroups = blocks;
+    e.waves = double(blocks) / (CUS * 8.0);
+    e.efficiency = 1.0;
+    e.cost = 1.0;
+    return e;
+  }
+  const std::uint64_t tm = (d.m + k.bm - 1) / k.bm, tn = (d.n + k.bn - 1) / k.bn;
+  const std::uint64_t tiles = tm * tn, slots = std::uint64_t(CUS) * resident(k);
+  const double rounds = std::ceil(double(tiles) / double(slots));
+  e.workgroups = tiles;
+  e.waves = double(tiles) / double(slots);
+  // Time: rounds of resident tiles, each round a tile's k-loop at the shape's rate (resident tiles share a CU).
+  e.cost = rounds * double(k.bm) * double(k.bn) * resident(k) / shape_rate(k);
+  const double useful = double(d.m) * double(d.n);
+  e.efficiency = useful / (rounds * double(slots) * double(k.bm) * double(k.bn)) * shape_rate(k);
+  return e;
+}
+
+// The kernel for a checked problem: the named one if it can run it, else the cheapest tiled kernel that fits, else
+// the skinny kernel for a decode-shaped bf16 problem, else the generic kernel.
+int choose(const cairn_gemm_desc& d, int named) {
+  if(named) {
+    if(named < 1 || named > COUNT) return -CAIRN_E_KERNEL;
+    const Kernel& k = TABLE[named - 1];
+    if(k.family == GENERIC) return named;
+    if(k.family == SKINNY) return skinny_fits(d) && d.c_type != CAIRN_TYPE_I32 ? named : -CAIRN_E_KERNEL;
+    return mfma_fits(d, k) ? named : -CAIRN_E_KERNEL;
+  }
+  if(d.m <= 16 && skinny_fits(d)) {
+    for(int id = 1; id <= COUNT; ++id)
+      if(TABLE[id - 1].family == SKINNY) return id;
+  }
+  int best = 0;
+  double cost = 0;
+  for(int id = 1; id <= COUNT; ++id) {
+    const Kernel& k = TABLE[id - 1];
+    if(!mfma_fits(d, k)) continue;
+    const double c = estimate(d, k).cost;
+    if(!best || c < cost) best = id, cost = c;
+  }
+  if(best) return best;
+  for(int id = 1; id <= COUNT; ++id)
+    if(TABLE[id - 1].family == GENERIC) return id;
+  return -CAIRN_E_KERNEL;
+}
+
+Params params_of(const cairn_gemm_desc& d, const Kernel& k) {
+  Params p{};
+  p.a = d.a;
+  p.b = d.b;
+  p.c = d.c;
+  p.lda = std::int64_t(d.lda);
+  p.ldb = std::int64_t(d.ldb);
+  p.ldc = std::int64_t(d.ldc);
+  p.m = int(d.m);
+  p.n = int(d.n);
+  p.k = int(d.k);
+  p.tiles_m = int((d.m + k.bm - 1) / k.bm);
+  p.tiles_n = int((d.n + k.bn - 1) / k.bn);
+  p.group = 4;
+  p.trans_a = d.trans_a;
+  p.trans_b = d.trans_b;
+  p.a_type = d.ab_type;
+  p.c_type = d.c_type;
+  p.accumulate = d.accumulate;
+  p.act = d.act;
+  p.bias = d.bias;
+  p.bias_type = d.bias_type;
+  p.row_scale = d.row_scale;
+  p.col_scale = d.col_scale;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char cairn_interface_gemm_gfx950_1[] = "cairn_gemm_gfx950";
+
+int cairn_gemm_kernel_count(void) { return COUNT; }
+
+int cairn_gemm_kernel_info(int32_t id, cairn_gemm_kernel* out) {
+  if(id < 1 || id > COUNT || !out) return CAIRN_E_KERNEL;
+  const Kernel& k = TABLE[id - 1];
+  std::memset(out, 0, sizeof(*out));
+  out->id = id;
+  out->ab_type = k.op == cairn::gemm::OP_BF16 ? CAIRN_TYPE_BF16
+                 : k.op == cairn::gemm::OP_F16 ? CAIRN_TYPE_F16
+                 : k.op == cairn::gemm::OP_I8  ? CAIRN_TYPE_I8
+                                               : -1;
+  out->trans_a = k.ta;
+  out->trans_b = k.tb;
+  out->tile_m = k.bm;
+  out->tile_n = k.bn;
+  out->tile_k = k.family == MFMA ? (k.op == cairn::gemm::OP_I8 ? 128 : 64) : (k.family == SKINNY ? 256 : 16);
+  out->threads = 256;
+  out->lds_bytes = k.family == MFMA ? 2 * (k.bm + k.bn) * 128 : (k.family == GENERIC ? 4096 : 0);
+  out->family = k.family;
+  std::strncpy(out->name, k.name, sizeof(out->name) - 1);
+  return CAIRN_OK;
+}
+
+const char* cairn_gemm_status_string(int status) {
+  switch(status) {
+    case CAIRN_OK: return "ok";
+    case CAIRN_E_SHAPE: return "an extent or leading dimension is out of range";
+    case CAIRN_E_TYPE: return "no kernel computes this combination of operand, output and bias types";
+    case CAIRN_E_KERNEL: return "the kernel named cannot run this problem";
+    case CAIRN_E_ARG: return "a required pointer is null or the descriptor is malformed";
+    case CAIRN_E_HIP: return "the HIP runtime refused the launch";
+    default: return "unknown status";
+  }
+}
+
+int cairn_gemm_select(const cairn_gemm_desc* desc, cairn_gemm_choice* out) {
+  Problem pr;
+  if(const int s = check(desc, pr)) return s;
+  const int id = choose(pr.d, desc->kernel);
+  if(id < 0) return -id;
+  if(out) {
+    const Kernel& k = TABLE[id - 1];
+    const Estimate e = estimate(pr.d, k);
+    std::memset(out, 0, sizeof(*out));
+    out->kernel = id;
+    out->family = k.family;
+    out->tile_m = k.bm;
+    out->tile_n = k.bn;
+    out->tile_k = k.family == MFMA ? (k.op == cairn::gemm::OP_I8 ? 128 : 64) : (k.family == SKINNY ? 256 : 16);
+    out->workgroups = e.workgroups;
+    out->waves = e.waves;
+    out->efficiency = e.efficiency;
+  }
+  return CAIRN_OK;
+}
+
+int cairn_gemm_run(const cairn_gemm_desc* desc, void* stream) {
+  Problem pr;
+  if(const int s = check(desc, pr)) return s;
+  const int id = choose(pr.d, desc->kernel);
+  if(id < 0) return -id;
+  if(pr.empty) return CAIRN_OK;
+  const Kernel& k = TABLE[id - 1];
+  const Params p = params_of(pr.d, k);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if(k.family == GENERIC) e = cairn_generic(p, s);
+  else if(k.family == SKINNY) e = cairn_skinny(p, s, 0);
+  else e = k.run(p, s);
+  return e == hipSuccess ? CAIRN_OK : CAIRN_E_HIP;
+}
+
+int cairn_gemm_mma(int32_t type, size_t m, size_t n, size_t k, float* c, const void* a, const void* b,
+                   void* stream) {
+  if(type != CAIRN_TYPE_F16 && type != CAIRN_TYPE_BF16 && type != CAIRN_TYPE_F8E4M3 && type != CAIRN_TYPE_F8E5M2)
+    return CAIRN_E_TYPE;
+  cairn_gemm_desc d{};
+  d.version = CAIRN_GEMM_DESC_VERSION;
+  d.ab_type = type;
+  d.c_type = CAIRN_TYPE_F32;
+  d.m = m;
+  d.n = n;
+  d.k = k;
+  d.a = a;
+  d.b = b;
+  d.c = c;
+  d.accumulate = 1;
+  return cairn_gemm_run(&d, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// What every GEMM kernel of the library takes, and the epilogue they all share: the per-launch parameters, the
+// output roundings and the fused bias / activation / dequant-scale step. Device code only; the host side of the
+// library (capi.cpp) fills a Params from a cairn_gemm_desc.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include "../../include/cairn_gemm.h"
+
+namespace cairn::gemm {
+
+// The matrix-core operations the tiled kernels run on.
+enum Op { OP_BF16 = 0, OP_F16 = 1, OP_I8 = 2 };
+
+// One launch. Matrices are the caller's: a is m x k (trans_a: stored k x m), b is k x n (trans_b: stored n x k), c
+// is m x n; ld* count elements between stored rows. Extents fit int32 (the host checks).
+struct Params {
+  const void* a;
+  const void* b;
+  void* c;
+  std::int64_t lda, ldb, ldc;
+  int m, n, k;
+  int tiles_m, tiles_n;  // the output tiles, for kernels that tile
+  int group;             // tile rows walked together for L2 reuse
+  int trans_a, trans_b;  // a stored k x m; b stored n x k
+  int a_type;            // CAIRN_TYPE_* of both operands
+  int c_type;            // CAIRN_TYPE_* of the output
+  int accumulate;        // f32 output: c = c_old + result
+  int act;               // CAIRN_ACT_*
+  const void* bias;      // per column, or null
+  int bias_type;         // CAIRN_TYPE_F32 or CAIRN_TYPE_BF16
+  const float* row_scale;
+  const float* col_scale;
+};
+
+__device__ inline std::uint32_t as_bits(float x) { return __builtin_bit_cast(std::uint32_t, x); }
+__device__ inline float from_bits(std::uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// f32 -> bf16, round to nearest even; past the largest finite value infinity; a NaN becomes the quiet NaN 0x7fc0
+// with its sign. These are the rules of the reference's narrow<bf16> (src/cairn/runtime/cairn_float.hpp:100-110),
+// applied to an f32, which is exact as a double.
+__device__ inline std::uint16_t narrow_bf16(float x) {
+  const std::uint32_t u = as_bits(x);
+  if((u & 0x7fffffffu) > 0x7f800000u) return std::uint16_t(((u >> 16) & 0x8000u) | 0x7fc0u);
+  return std::uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+// f32 -> f16, round to nearest even (the conversion's mode), overflow to infinity.
+__device__ inline std::uint16_t narrow_f16(float x) {
+  const _Float16 h = static_cast<_Float16>(x);
+  return __builtin_bit_cast(std::uint16_t, h);
+}
+__device__ inline float widen_bf16(std::uint16_t b) { return from_bits(std::uint32_t(b) << 16); }
+
+// GELU in its erf form, 0.5 x (1 + erf(x / sqrt 2)), in f32.
+__device__ inline float gelu(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
+
+// The epilogue of the outputs (m, n0 .. n0+count-1) of one row, on f32 values v: each step an f32 rounding, in this
+// order: times row_scale[m], times col_scale[n], plus bias[n], the activation, then (f32 output with accumulate)
+// plus the old value. A NaN passes ReLU as a NaN.
+template<int COUNT> __device__ inline void epilogue(const Params& p, int m, int n0, float (&v)[COUNT]) {
+  if(p.row_scale) {
+    const float s = p.row_scale[m];
+    for(int t = 0; t < COUNT; ++t) v[t] = v[t] * s;
+  }
+  if(p.col_scale)
+    for(int t = 0; t < COUNT; ++t) v[t] = v[t] * p.col_scale[n0 + t];
+  if(p.bias) {
+    if(p.bias_type == CAIRN_TYPE_BF16) {
+      const std::uint16_t* b = static_cast<const std::uint16_t*>(p.bias);
+      for(int t = 0; t < COUNT; ++t) v[t] = v[t] + widen_bf16(b[n0 + t]);
+    } else {
+      const float* b = static_cast<const float*>(p.bias);
+      for(int t = 0; t < COUNT; ++t) v[t] = v[t] + b[n0 + t];
+    }
+  }
+  if(p.act == CAIRN_ACT_RELU)
+    for(int t = 0; t < COUNT; ++t) v[t] = v[t] < 0.0f ? 0.0f : v[t];
+  else if(p.act == CAIRN_ACT_GELU)
+    for(int t = 0; t < COUNT; ++t) v[t] = gelu(v[t]);
+}
+
+}  // namespace cairn::gemm

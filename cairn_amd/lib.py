@@ -1,0 +1,178 @@
+"""ctypes bindings of libcairn_gemm_gfx950.so, the library include/cairn_gemm.h declares.
+
+The library is the product: there is no fallback. If it has not been built (python -m cairn_amd.build), loading
+raises LibraryMissing, and every entry that would run on the GPU fails with it.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / "libcairn_gemm_gfx950.so"
+
+# enum cairn_type, cairn_act, cairn_status
+F32, F16, BF16, F8E4M3, F8E5M2, I8, I32 = range(7)
+ACT_NONE, ACT_RELU, ACT_GELU = range(3)
+OK, E_SHAPE, E_TYPE, E_KERNEL, E_ARG, E_HIP = range(6)
+DESC_VERSION = 1
+FAMILY = {0: "mfma", 1: "generic", 2: "skinny"}
+TYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", F8E4M3: "f8e4m3", F8E5M2: "f8e5m2", I8: "i8", I32: "i32"}
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+class GemmError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"cairn_gemm: {message} (status {status})")
+        self.status = status
+
+
+class Desc(C.Structure):
+    """struct cairn_gemm_desc."""
+
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("ab_type", C.c_int32),
+        ("c_type", C.c_int32),
+        ("trans_a", C.c_int32),
+        ("trans_b", C.c_int32),
+        ("m", C.c_uint64),
+        ("n", C.c_uint64),
+        ("k", C.c_uint64),
+        ("lda", C.c_uint64),
+        ("ldb", C.c_uint64),
+        ("ldc", C.c_uint64),
+        ("a", C.c_void_p),
+        ("b", C.c_void_p),
+        ("c", C.c_void_p),
+        ("accumulate", C.c_int32),
+        ("act", C.c_int32),
+        ("bias", C.c_void_p),
+        ("bias_type", C.c_int32),
+        ("row_scale", C.c_void_p),
+        ("col_scale", C.c_void_p),
+        ("kernel", C.c_int32),
+    ]
+
+
+class Kernel(C.Structure):
+    """struct cairn_gemm_kernel."""
+
+    _fields_ = [
+        ("id", C.c_int32),
+        ("ab_type", C.c_int32),
+        ("trans_a", C.c_int32),
+        ("trans_b", C.c_int32),
+        ("tile_m", C.c_int32),
+        ("tile_n", C.c_int32),
+        ("tile_k", C.c_int32),
+        ("threads", C.c_int32),
+        ("lds_bytes", C.c_int32),
+        ("family", C.c_int32),
+        ("name", C.c_char * 48),
+    ]
+
+
+class Choice(C.Structure):
+    """struct cairn_gemm_choice."""
+
+    _fields_ = [
+        ("kernel", C.c_int32),
+        ("family", C.c_int32),
+        ("tile_m", C.c_int32),
+        ("tile_n", C.c_int32),
+        ("tile_k", C.c_int32),
+        ("workgroups", C.c_uint64),
+        ("waves", C.c_double),
+        ("efficiency", C.c_double),
+    ]
+
+
+# Every symbol include/cairn_gemm.h declares, with its ctypes signature.
+SZ = C.c_size_t
+_MMA = [SZ, SZ, SZ, SZ, C.c_void_p, SZ, C.c_void_p, SZ, C.c_void_p]
+SIGNATURES = {
+    "cairn_gemm_run": (C.c_int, [C.POINTER(Desc), C.c_void_p]),
+    "cairn_gemm_select": (C.c_int, [C.POINTER(Desc), C.POINTER(Choice)]),
+    "cairn_gemm_kernel_count": (C.c_int, []),
+    "cairn_gemm_kernel_info": (C.c_int, [C.c_int32, C.POINTER(Kernel)]),
+    "cairn_gemm_status_string": (C.c_char_p, [C.c_int]),
+    "cairn_gemm_mma": (C.c_int, [C.c_int32, SZ, SZ, SZ, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "cairn_gemm_device_stream": (None, [C.c_void_p]),
+    **{f"cf_mma_{f}": (None, _MMA) for f in ("f32", "f16", "bf16", "f8e4m3", "f8e5m2")},
+    **{f"cf_mma_{f}_device": (None, _MMA) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
+    **{f"cq_mma_{f}_device": (None, [C.c_void_p, *_MMA]) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
+}
+DATA_SYMBOLS = ["cairn_interface_gemm_gfx950_1"]
+
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """The library, loaded once, every declared entry typed. Raises LibraryMissing if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise LibraryMissing(f"{LIBRARY} is not built: run `python -m cairn_amd.build` (hipcc, gfx950)")
+        lib = C.CDLL(str(LIBRARY))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(lib, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return load().cairn_gemm_status_string(status).decode()
+
+
+def desc(ab_type: int, c_type: int, m: int, n: int, k: int, a=None, b=None, c=None, *, trans_a: bool = False,
+         trans_b: bool = False, lda: int = 0, ldb: int = 0, ldc: int = 0, accumulate: bool = False,
+         act: int = ACT_NONE, bias=None, bias_type: int = F32, row_scale=None, col_scale=None,
+         kernel: int = 0) -> Desc:  # fmt: skip
+    """A cairn_gemm_desc; pointers are ints (device addresses) or None."""
+    return Desc(DESC_VERSION, ab_type, c_type, int(trans_a), int(trans_b), m, n, k, lda, ldb, ldc, a, b, c,
+                int(accumulate), act, bias, bias_type, row_scale, col_scale, kernel)  # fmt: skip
+
+
+def run(d: Desc, stream: int | None = None) -> None:
+    s = load().cairn_gemm_run(C.byref(d), stream)
+    if s != OK:
+        raise GemmError(s, status_string(s))
+
+
+def select(d: Desc) -> dict:
+    choice = Choice()
+    s = load().cairn_gemm_select(C.byref(d), C.byref(choice))
+    if s != OK:
+        raise GemmError(s, status_string(s))
+    info = kernel_info(choice.kernel)
+    return {"kernel": choice.kernel, "name": info["name"], "family": FAMILY[choice.family], "tile_m": choice.tile_m,
+            "tile_n": choice.tile_n, "tile_k": choice.tile_k, "workgroups": choice.workgroups,
+            "waves": choice.waves, "efficiency": choice.efficiency}  # fmt: skip
+
+
+def kernel_info(kid: int) -> dict:
+    k = Kernel()
+    s = load().cairn_gemm_kernel_info(kid, C.byref(k))
+    if s != OK:
+        raise GemmError(s, status_string(s))
+    return {"id": k.id, "name": k.name.decode(), "ab_type": k.ab_type, "trans_a": bool(k.trans_a),
+            "trans_b": bool(k.trans_b), "tile_m": k.tile_m, "tile_n": k.tile_n, "tile_k": k.tile_k,
+            "threads": k.threads, "lds_bytes": k.lds_bytes, "family": FAMILY[k.family]}  # fmt: skip
+
+
+def kernels() -> list[dict]:
+    return [kernel_info(i) for i in range(1, load().cairn_gemm_kernel_count() + 1)]
+
+
+def kernel_named(name: str) -> int:
+    for k in kernels():
+        if k["name"] == name:
+            return k["id"]
+    raise KeyError(name)

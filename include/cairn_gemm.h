@@ -1,0 +1,179 @@
+/*
+ * cairn_gemm.h: the C ABI of libcairn_gemm_gfx950.so, the MI355X (gfx950) tensor-core GEMM library behind CAIRN's
+ * mma_unordered. Plain C: pointers, sizes and one descriptor struct; no HIP or C++ types cross it. A stream is a
+ * hipStream_t passed as void* (NULL: the null stream).
+ *
+ * Two layers:
+ *
+ * 1. The entries a CAIRN library would export for the multiply, with the spellings CAIRN's C header generator gives
+ *    them (src/cairn/compiler/lower/header.py:215-249, 283-313): cf_NAME is the checked synchronous entry,
+ *    cq_NAME(stream, ...) the same work queued on the caller's stream, NAME_device_stream binds the calling thread's
+ *    synchronous device work to a caller-owned stream. They are the functions tests/soundness/test_tensor.py:31-36
+ *    compiles around mma_unordered, one per storage float, for host views (cf_mma_<fmt>: the reference loop,
+ *    cr::tensor::multiply, src/cairn/runtime/cairn_tensor.hpp:37-41) and device views (cf_mma_<fmt>_device,
+ *    cq_mma_<fmt>_device: cr::tensor::launch, cairn_tensor.hpp:206-221). c += a * b with a m x k and b k x n
+ *    row-major, c m x n row-major f32; the extents must agree with the view lengths or the process aborts.
+ *
+ * 2. The general entry the C++ runtime (include/cairn/cairn_tensor.hpp) calls: cairn_gemm_run with a descriptor
+ *    that adds what the reference lacks: NT/TN/TT layouts, leading dimensions, bf16/f16/int32 outputs, a fused
+ *    epilogue (per-row and per-column scales, bias, ReLU/GELU), int8 operands (W8A8), and the kernel choice the
+ *    tile selector makes (cairn_gemm_select), which the perf model reads.
+ *
+ * Numerics: the reference contract (src/cairn/compiler/device/tensor.py:1-18, docs/numerics.md:53-78): every product
+ * exact in f32, every output its old value plus its k products in an order the hardware picks, within
+ * (k + 1) * 2^-22 * (|c| + sum |a * b|) of the exact sum. Two runs on one device give the same bits: no kernel here
+ * reduces through atomics. int8 products accumulate exactly in int32.
+ */
+#ifndef CAIRN_GEMM_H
+#define CAIRN_GEMM_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage floats as the C header states them (header.py:276-277): the pattern and nothing else. */
+typedef struct { uint16_t bits; } cairn_f16;
+typedef struct { uint16_t bits; } cairn_bf16;
+typedef struct { uint8_t bits; } cairn_f8e4m3;
+typedef struct { uint8_t bits; } cairn_f8e5m2;
+
+enum cairn_type {
+  CAIRN_TYPE_F32 = 0,
+  CAIRN_TYPE_F16 = 1,
+  CAIRN_TYPE_BF16 = 2,
+  CAIRN_TYPE_F8E4M3 = 3,
+  CAIRN_TYPE_F8E5M2 = 4,
+  CAIRN_TYPE_I8 = 5,
+  CAIRN_TYPE_I32 = 6
+};
+
+enum cairn_act { CAIRN_ACT_NONE = 0, CAIRN_ACT_RELU = 1, CAIRN_ACT_GELU = 2 };
+
+enum cairn_status {
+  CAIRN_OK = 0,
+  CAIRN_E_SHAPE = 1,   /* an extent is negative-free but too large, or a leading dimension too small */
+  CAIRN_E_TYPE = 2,    /* an operand/output/bias type combination no kernel computes */
+  CAIRN_E_KERNEL = 3,  /* the kernel id named does not exist or cannot run this problem */
+  CAIRN_E_ARG = 4,     /* a null pointer where data is needed, or a bad descriptor version */
+  CAIRN_E_HIP = 5      /* the HIP runtime refused the launch */
+};
+
+#define CAIRN_GEMM_DESC_VERSION 1u
+
+/*
+ * One GEMM: c = epilogue(a * b). a is m x k, stored row-major (trans_a = 0) or as its transpose, k x m row-major
+ * (trans_a = 1); b is k x n, stored row-major (trans_b = 0) or as its transpose, n x k (trans_b = 1). So the
+ * forward layer X.W is NN, dX = dY.W^T is NT (b = W read K-contiguous) and dW = X^T.dY is TN. c is m x n row-major.
+ * A leading dimension of 0 means packed. The epilogue, each step an f32 rounding, in order:
+ *   v = acc                            (f32; int8: the exact int32 sum converted to f32, nearest even)
+ *   v = v * row_scale[i]               if row_scale
+ *   v = v * col_scale[j]               if col_scale
+ *   v = v + bias[j]                    if bias (f32 or bf16)
+ *   v = relu(v) or gelu(v)             per act (GELU: 0.5 v (1 + erf(v / sqrt 2)))
+ *   v = c_old + v                      if c_type is F32 and accumulate (the reference's c += a * b)
+ * and stored as c_type: F32, BF16 or F16 (nearest even, overflow to infinity), or I32 (int8 operands with no
+ * epilogue: the accumulator itself, bit-exact).
+ */
+typedef struct cairn_gemm_desc {
+  uint32_t version; /* CAIRN_GEMM_DESC_VERSION */
+  int32_t ab_type;  /* F16, BF16, F8E4M3, F8E5M2 or I8, for both operands */
+  int32_t c_type;   /* F32, BF16, F16 or I32 */
+  int32_t trans_a, trans_b;
+  uint64_t m, n, k;
+  uint64_t lda, ldb, ldc;
+  const void* a;
+  const void* b;
+  void* c;
+  int32_t accumulate;
+  int32_t act;
+  const void* bias;
+  int32_t bias_type; /* F32 or BF16 */
+  const float* row_scale;
+  const float* col_scale;
+  int32_t kernel; /* 0: the selector's choice; else an id cairn_gemm_kernel_info knows */
+} cairn_gemm_desc;
+
+/* A kernel of the library: its id, what it computes and the tile it runs. */
+typedef struct cairn_gemm_kernel {
+  int32_t id;
+  int32_t ab_type;       /* operand type it computes (F16 covers the widened 8-bit floats) */
+  int32_t trans_a, trans_b;
+  int32_t tile_m, tile_n, tile_k; /* output tile and k-step, in elements */
+  int32_t threads;       /* per workgroup */
+  int32_t lds_bytes;     /* per workgroup */
+  int32_t family;        /* 0: MFMA tiled, 1: generic (any shape), 2: skinny (m <= 16, bandwidth) */
+  char name[48];
+} cairn_gemm_kernel;
+
+/* The selector's answer for one problem: the kernel and the work it launches. */
+typedef struct cairn_gemm_choice {
+  int32_t kernel;        /* id */
+  int32_t family;
+  int32_t tile_m, tile_n, tile_k;
+  uint64_t workgroups;   /* launched */
+  double waves;          /* workgroups / (CUs x workgroups resident per CU) */
+  double efficiency;     /* the share of the machine the tiling keeps busy: whole-wave and edge-tile losses */
+} cairn_gemm_choice;
+
+/* Queue the GEMM on `stream`. Returns without waiting, allocates nothing and makes no stream or event, so it may be
+ * captured in a HIP graph. A nonzero status means nothing was queued (CAIRN_E_HIP: the launch itself failed). */
+int cairn_gemm_run(const cairn_gemm_desc* d, void* stream);
+
+/* The kernel cairn_gemm_run would launch for `d` (d->kernel 0) or checks that d->kernel can run it. No GPU call. */
+int cairn_gemm_select(const cairn_gemm_desc* d, cairn_gemm_choice* out);
+
+/* The kernel table: count, and the entry for one id (1 .. count). */
+int cairn_gemm_kernel_count(void);
+int cairn_gemm_kernel_info(int32_t id, cairn_gemm_kernel* out);
+
+/* A static description of a status code. */
+const char* cairn_gemm_status_string(int status);
+
+/* The reference's whole-matrix device multiply on a stream: c += a * b, a m x k and b k x n row-major storage floats
+ * of `type` (F16, BF16, F8E4M3, F8E5M2), c m x n row-major f32. What cr::tensor::launch<A> queues
+ * (cairn_tensor.hpp:206-221); m, n or k of 0 queues nothing (k = 0 leaves c as it is). */
+int cairn_gemm_mma(int32_t type, size_t m, size_t n, size_t k, float* c, const void* a, const void* b, void* stream);
+
+/* The multiply's CAIRN entries (layer 1 above). cf_mma_<fmt> runs on the host, the reference loop; the device
+ * variants run on the calling thread's execution context (synchronous: they return once their own stream has run
+ * the work) and the cq_ variants queue on the caller's stream without waiting. cf_mma_f32 is the f32 instance of
+ * the host template (config C1); the reference's checker refuses f32 operands (E-MMA) but its template computes it. */
+void cf_mma_f32(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const float* a, size_t bn,
+                const float* b);
+void cf_mma_f16(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_f16* a, size_t bn,
+                const cairn_f16* b);
+void cf_mma_bf16(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_bf16* a, size_t bn,
+                 const cairn_bf16* b);
+void cf_mma_f8e4m3(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_f8e4m3* a, size_t bn,
+                   const cairn_f8e4m3* b);
+void cf_mma_f8e5m2(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_f8e5m2* a, size_t bn,
+                   const cairn_f8e5m2* b);
+void cf_mma_f16_device(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_f16* a, size_t bn,
+                       const cairn_f16* b);
+void cf_mma_bf16_device(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_bf16* a,
+                        size_t bn, const cairn_bf16* b);
+void cf_mma_f8e4m3_device(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_f8e4m3* a,
+                          size_t bn, const cairn_f8e4m3* b);
+void cf_mma_f8e5m2_device(size_t m, size_t n, size_t k, size_t cn, float* c, size_t an, const cairn_f8e5m2* a,
+                          size_t bn, const cairn_f8e5m2* b);
+void cq_mma_f16_device(void* stream, size_t m, size_t n, size_t k, size_t cn, float* c, size_t an,
+                       const cairn_f16* a, size_t bn, const cairn_f16* b);
+void cq_mma_bf16_device(void* stream, size_t m, size_t n, size_t k, size_t cn, float* c, size_t an,
+                        const cairn_bf16* a, size_t bn, const cairn_bf16* b);
+void cq_mma_f8e4m3_device(void* stream, size_t m, size_t n, size_t k, size_t cn, float* c, size_t an,
+                          const cairn_f8e4m3* a, size_t bn, const cairn_f8e4m3* b);
+void cq_mma_f8e5m2_device(void* stream, size_t m, size_t n, size_t k, size_t cn, float* c, size_t an,
+                          const cairn_f8e5m2* a, size_t bn, const cairn_f8e5m2* b);
+
+/* The calling thread's synchronous device work runs on `stream`, a hipStream_t the caller owns and keeps alive, after
+ * what the caller queued there; NULL gives the thread its own stream back (header.py:296-304, cairn_exec.hpp:38-41). */
+void cairn_gemm_device_stream(void* stream);
+
+/* The interface identity: defined by the library built with this header (header.py:280-285). */
+extern const char cairn_interface_gemm_gfx950_1[];
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CAIRN_GEMM_H */

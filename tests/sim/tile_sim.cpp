@@ -1,0 +1,307 @@
+// The gfx950 MFMA tile run on the host: every thread's fetches, transposes and LDS writes through the very code the
+// kernel runs (cairn_amd/csrc/tile.hpp), every lane's fragment reads, a model of the matrix core, and the epilogue's
+// output mapping. It holds the kernel's index arithmetic to four rules, for every layout, tile shape and operand size,
+// on shapes with tails in every direction and padded leading dimensions:
+//
+//   1. every global load the kernel makes either lies wholly inside its matrix's allocation or is one the hardware
+//      turns into zeros (an offset past the buffer resource), and no load straddles the resource's end;
+//   2. every 16-byte chunk of an LDS stage is written exactly once per k-step, inside the stage;
+//   3. every output element is written exactly once, and none outside the matrix;
+//   4. the outputs equal the exact product (values chosen so every sum is exact), old values added.
+//
+// The matrix-core model: lane l supplies row l%32 of its operand and 16 bytes of k (chunk 2s + l/32); the output of
+// register r of lane l is row 8(r/4) + 4(l/32) + r%4 of the first operand, column l%32 of the second. The GPU tests
+// check the model against the hardware; this program checks everything around it. Mirrors, in spirit, the
+// reference's host run of its device tile (tests/runtime/tensor_runtime.cpp).
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+#include "tile.hpp"
+
+using namespace cairn::tile;
+
+namespace {
+
+int failures = 0;
+#define FAIL(...)                 \
+  do {                            \
+    std::printf(__VA_ARGS__);     \
+    std::printf("\n");            \
+    ++failures;                   \
+    return;                       \
+  } while(0)
+
+std::uint64_t mix(std::uint64_t x) {
+  x ^= x >> 31;
+  x *= 0x7fb5d329728ea185ULL;
+  x ^= x >> 27;
+  x *= 0x94d049bb133111ebULL;
+  x ^= x >> 29;
+  return x;
+}
+
+// Checked memory: a load must lie inside the resource or be wholly past it; a load inside the resource must lie
+// inside the allocation the matrix came from.
+struct HostMem {
+  const char* lo;
+  const char* hi;
+  bool bad = false;
+  struct Rsrc {
+    const char* base;
+    std::int64_t bytes;
+  };
+  Rsrc resource(const char* base, std::int64_t bytes) {
+    return Rsrc{base, bytes < 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffffLL : bytes)};
+  }
+  template<int N> void read(Rsrc r, int off, std::uint32_t* out) {
+    std::memset(out, 0, N);
+    if(off < 0) bad = true;
+    if(off >= r.bytes) return;  // the hardware's zeros
+    if(std::int64_t(off) + N > r.bytes) bad = true;  // straddles the resource's end
+    const char* at = r.base + off;
+    if(at < lo || at + N > hi) {
+      bad = true;
+      return;
+    }
+    std::memcpy(out, at, N);
+  }
+  u32x4 load16(Rsrc r, int off) {
+    std::uint32_t w[4];
+    read<16>(r, off, w);
+    return u32x4{w[0], w[1], w[2], w[3]};
+  }
+  u32x2 load8(Rsrc r, int off) {
+    std::uint32_t w[2];
+    read<8>(r, off, w);
+    return u32x2{w[0], w[1]};
+  }
+};
+
+struct HostLds {
+  std::vector<std::uint8_t> bytes;
+  std::vector<int> writes;  // per 16-byte chunk
+  bool bad = false;
+  explicit HostLds(int size) : bytes(size), writes(size / 16) {}
+  void write16(int off, u32x4 v) {
+    if(off < 0 || off % 16 || off + 16 > int(bytes.size())) {
+      bad = true;
+      return;
+    }
+    std::memcpy(&bytes[off], &v, 16);
+    ++writes[off / 16];
+  }
+};
+
+// Operand values: bf16 (a multiple of 1/16 in [-1.875, 1.875]) or int8 in [-127, 127]; the element is written into
+// the stored matrix at `at`.
+template<int ES> double value_of(const std::vector<std::uint8_t>& m, std::int64_t at) {
+  if constexpr(ES == 2) {
+    std::uint16_t b;
+    std::memcpy(&b, &m[at * 2], 2);
+    const std::uint32_t u = std::uint32_t(b) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+  } else {
+    return double(std::int8_t(m[at]));
+  }
+}
+template<int ES> void put(std::vector<std::uint8_t>& m, std::int64_t at, std::uint64_t h) {
+  if constexpr(ES == 2) {
+    const float f = float(std::int64_t(h % 61) - 30) / 16.0f;  // exact in bf16
+    std::uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const std::uint16_t b = std::uint16_t(u >> 16);
+    std::memcpy(&m[at * 2], &b, 2);
+  } else {
+    m[at] = std::uint8_t(std::int8_t(std::int64_t(h % 255) - 127));
+  }
+}
+// A chunk's elements as values.
+template<int ES> void decode(const std::uint8_t* chunk, double* out) {
+  for(int e = 0; e < 16 / ES; ++e) {
+    if constexpr(ES == 2) {
+      std::uint16_t b;
+      std::memcpy(&b, chunk + 2 * e, 2);
+      const std::uint32_t u = std::uint32_t(b) << 16;
+      float f;
+      std::memcpy(&f, &u, 4);
+      out[e] = f;
+    } else {
+      out[e] = double(std::int8_t(chunk[e]));
+    }
+  }
+}
+
+template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k, int pad, int group) {
+  using Sh = Shape<BM, BN, ES>;
+  constexpr bool AK = !TA, BK_ = TB;
+  const char* lay = TA ? (TB ? "TT" : "TN") : (TB ? "NT" : "NN");
+  // Stored matrices, padded: a is m x k (TA: k x m), b is k x n (TB: n x k).
+  const std::int64_t lda = (TA ? m : k) + pad, ldb = (TB ? k : n) + pad, ldc = n + pad;
+  const std::int64_t arows = TA ? k : m, brows = TB ? n : k;
+  const std::int64_t abytes = std::max<std::int64_t>(1, ((arows ? arows - 1 : 0) * lda + (TA ? m : k)) * ES);
+  const std::int64_t bbytes = std::max<std::int64_t>(1, ((brows ? brows - 1 : 0) * ldb + (TB ? k : n)) * ES);
+  std::vector<std::uint8_t> A(abytes, 0x7f), B(bbytes, 0x7f);  // padding: 0x7f7f is a huge bf16, 127 an int8
+  for(std::int64_t r = 0; r < arows; ++r)
+    for(int q = 0; q < (TA ? m : k); ++q) put<ES>(A, r * lda + q, mix(11 + r * 7919 + q));
+  for(std::int64_t r = 0; r < brows; ++r)
+    for(int q = 0; q < (TB ? k : n); ++q) put<ES>(B, r * ldb + q, mix(23 + r * 104729 + q));
+  auto a_at = [&](int i, int p) { return TA ? std::int64_t(p) * lda + i : std::int64_t(i) * lda + p; };
+  auto b_at = [&](int p, int j) { return TB ? std::int64_t(j) * ldb + p : std::int64_t(p) * ldb + j; };
+
+  std::vector<double> C(std::size_t(m) * ldc), old(std::size_t(m) * ldc);
+  std::vector<int> written(std::size_t(m) * ldc);
+  for(std::size_t e = 0; e < C.size(); ++e) C[e] = old[e] = double(std::int64_t(mix(99 + e) % 9) - 4) / 4.0;
+
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN, total = tiles_m * tiles_n;
+  std::vector<int> seen(total);
+  HostMem mem_a{reinterpret_cast<const char*>(A.data()), reinterpret_cast<const char*>(A.data()) + A.size()};
+  HostMem mem_b{reinterpret_cast<const char*>(B.data()), reinterpret_cast<const char*>(B.data()) + B.size()};
+  for(int wg = 0; wg < total; ++wg) {
+    int tm, tn;
+    tile_of(wg, tiles_m, tiles_n, group, tm, tn);
+    if(tm < 0 || tm >= tiles_m || tn < 0 || tn >= tiles_n) FAIL("%s tile_of(%d) = (%d, %d) off the grid", lay, wg, tm, tn);
+    ++seen[tm * tiles_n + tn];
+    const int row0 = tm * BM, col0 = tn * BN;
+    const Panel pa = panel(AK, row0, m, k, lda, ES), pb = panel(BK_, col0, n, k, ldb, ES);
+    std::vector<Operand<Sh, BM, AK, HostMem>> fa(Sh::THREADS);
+    std::vector<Operand<Sh, BN, BK_, HostMem>> fb(Sh::THREADS);
+    for(int t = 0; t < Sh::THREADS; ++t) {
+      fa[t].setup(t, row0, m, lda);
+      fb[t].setup(t, col0, n, ldb);
+    }
+    std::vector<double> acc(static_cast<std::size_t>(BM * BN), 0.0);  // by output (row, column) of the tile
+    const int steps = (k + Sh::BK - 1) / Sh::BK;
+    for(int kt = 0; kt < steps; ++kt) {
+      HostLds lds(Sh::STAGE);
+      for(int t = 0; t < Sh::THREADS; ++t) {
+        fa[t].fetch(mem_a, reinterpret_cast<const char*>(A.data()), pa, lda, kt, k, t);
+        fb[t].fetch(mem_b, reinterpret_cast<const char*>(B.data()), pb, ldb, kt, k, t);
+        fa[t].store(lds, 0, t);
+        fb[t].store(lds, Sh::A_BYTES, t);
+      }
+      if(mem_a.bad || mem_b.bad) FAIL("%s %dx%d es=%d %dx%dx%d: a global load outside its matrix", lay, BM, BN, ES, m, n, k);
+      if(lds.bad) FAIL("%s %dx%d: an LDS write off the stage", lay, BM, BN);
+      for(int c = 0; c < Sh::STAGE / 16; ++c)
+        if(lds.writes[c] != 1) FAIL("%s %dx%d es=%d: LDS chunk %d written %d times", lay, BM, BN, ES, c, lds.writes[c]);
+      // The matrix core, wave by wave: first operand the B block (rows = n), second the A block (columns = m).
+      for(int w = 0; w < 4; ++w) {
+        const int wm = w / Sh::WAVES_N, wn = w % Sh::WAVES_N;
+        for(int s = 0; s < Sh::STEPS; ++s)
+          for(int i = 0; i < Sh::FM; ++i)
+            for(int j = 0; j < Sh::FN; ++j) {
+              double P[32][32], Q[32][32];  // P[row][kk], Q[kk][col], kk over this step's 32 bytes of k
+              constexpr int CE = 16 / ES;
+              for(int l = 0; l < 64; ++l) {
+                double pb_[16], qa_[16];
+                decode<ES>(&lds.bytes[Sh::A_BYTES + fragment_offset(wn * Sh::WTN + 32 * j, s, l)], pb_);
+                decode<ES>(&lds.bytes[fragment_offset(wm * Sh::WTM + 32 * i, s, l)], qa_);
+                for(int e = 0; e < CE; ++e) {
+                  P[l & 31][(l >> 5) * CE + e] = pb_[e];
+                  Q[(l >> 5) * CE + e][l & 31] = qa_[e];
+                }
+              }
+              for(int l = 0; l < 64; ++l)
+                for(int r = 0; r < 16; ++r) {
+                  const int prow = 8 * (r / 4) + 4 * (l / 32) + r % 4, qcol = l % 32;
+                  double sum = 0;
+                  for(int kk = 0; kk < 2 * CE; ++kk) sum += P[prow][kk] * Q[kk][qcol];
+                  // Output mapping of tile.hpp: lane l, quad q = r/4, element e = r%4.
+                  const int mm = wm * Sh::WTM + 32 * i + acc_m(l);
+                  const int nn = wn * Sh::WTN + 32 * j + acc_n(l, r / 4) + r % 4;
+                  if(mm != wm * Sh::WTM + 32 * i + qcol || nn != wn * Sh::WTN + 32 * j + prow)
+                    FAIL("%s: accumulator mapping disagrees with the matrix-core model", lay);
+                  acc[std::size_t(mm) * BN + nn] += sum;
+                }
+            }
+      }
+    }
+    // Epilogue: every output of the tile inside the matrix, once.
+    for(int w = 0; w < 4; ++w) {
+      const int wm = w / Sh::WAVES_N, wn = w % Sh::WAVES_N;
+      for(int i = 0; i < Sh::FM; ++i)
+        for(int j = 0; j < Sh::FN; ++j)
+          for(int l = 0; l < 64; ++l)
+            for(int q = 0; q < 4; ++q) {
+              const int mm = wm * Sh::WTM + 32 * i + acc_m(l), nn0 = wn * Sh::WTN + 32 * j + acc_n(l, q);
+              const int gm = row0 + mm, gn = col0 + nn0;
+              if(gm >= m || gn >= n) continue;
+              if(gn + 3 >= n + 3 && n % 4) FAIL("%s: a quad straddles n", lay);
+              for(int e = 0; e < 4; ++e) {
+                const std::size_t at = std::size_t(gm) * ldc + gn + e;
+                C[at] = old[at] + acc[std::size_t(mm) * BN + nn0 + e];
+                ++written[at];
+              }
+            }
+    }
+  }
+  for(int id = 0; id < total; ++id)
+    if(seen[id] != 1) FAIL("%s: tile %d computed %d times", lay, id, seen[id]);
+  for(int i = 0; i < m; ++i)
+    for(int j = 0; j < n; ++j) {
+      double want = old[std::size_t(i) * ldc + j];
+      double exact = 0;
+      for(int p = 0; p < k; ++p) exact += value_of<ES>(A, a_at(i, p)) * value_of<ES>(B, b_at(p, j));
+      want += exact;
+      const std::size_t at = std::size_t(i) * ldc + j;
+      if(written[at] != 1) FAIL("%s %dx%d es=%d %dx%dx%d: output (%d,%d) written %d times", lay, BM, BN, ES, m, n, k, i, j, written[at]);
+      if(C[at] != want)
+        FAIL("%s %dx%d es=%d %dx%dx%d pad %d: output (%d,%d) is %.9g, exact %.9g", lay, BM, BN, ES, m, n, k, pad, i, j,
+             C[at], want);
+    }
+}
+
+template<int BM, int BN, int ES> void layouts(int m, int n, int k, int pad, int group) {
+  run<BM, BN, ES, false, false>(m, n, k, pad, group);
+  run<BM, BN, ES, false, true>(m, n, k, pad, group);
+  run<BM, BN, ES, true, false>(m, n, k, pad, group);
+  run<BM, BN, ES, true, true>(m, n, k, pad, group);
+}
+
+template<int BM, int BN, int ES> void shapes() {
+  // m and n multiples of 8 (the MN-major fetch's 8-column pieces), k a multiple of the 16-byte chunk; tails in every
+  // direction against the tile and the k-step, padded and packed leading dimensions, one and several groups.
+  constexpr int CE = 16 / ES;
+  const int list[][5] = {{8, 8, CE, 0, 4},           {64, 64, 4 * CE, 8, 4},      {BM, BN, 128 / ES, 0, 4},
+                         {BM + 8, BN + 24, 3 * CE, 8, 1}, {2 * BM + 72, BN - 8, 200 / CE * CE, 16, 2},
+                         {264, 3 * BN + 8, 19 * CE, 0, 4}};
+  for(auto& s : list) layouts<BM, BN, ES>(s[0], s[1], s[2], s[3], s[4]);
+}
+
+}  // namespace
+
+int main() {
+  shapes<256, 256, 2>();
+  shapes<256, 128, 2>();
+  shapes<128, 256, 2>();
+  shapes<128, 128, 2>();
+  shapes<256, 256, 1>();
+  shapes<256, 128, 1>();
+  shapes<128, 128, 1>();
+  // tile_of is a bijection for grids whose size is and is not a multiple of 8, and for partial groups.
+  for(int tm = 1; tm <= 13; ++tm)
+    for(int tn = 1; tn <= 11; ++tn)
+      for(int g = 1; g <= 5; ++g) {
+        std::vector<int> seen(tm * tn);
+        for(int b = 0; b < tm * tn; ++b) {
+          int x, y;
+          tile_of(b, tm, tn, g, x, y);
+          if(x < 0 || x >= tm || y < 0 || y >= tn) {
+            std::printf("tile_of off the grid\n");
+            return 1;
+          }
+          ++seen[x * tn + y];
+        }
+        for(int v : seen)
+          if(v != 1) {
+            std::printf("tile_of is not a bijection at %d x %d group %d\n", tm, tn, g);
+            return 1;
+          }
+      }
+  if(failures) return 1;
+  std::printf("ok: every tile equals the exact product\n");
+  return 0;
+}

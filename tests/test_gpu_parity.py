@@ -1,0 +1,262 @@
+"""The gfx950 kernels against the oracle, through the C ABI (include/cairn_gemm.h).
+
+- The reference's own device shapes (tests/soundness/test_tensor.py:183-222) with its generator: values that are
+  multiples of 1/16, so every sum is exact in f32 and the device must equal the host reference loop bit for bit,
+  whatever order the matrix cores add in.
+- Random bf16/f16 operands on every layout and output type, held to the contract
+  |got - exact| <= (k + 1) 2^-22 (|c| + sum |a b|) (src/cairn/compiler/device/tensor.py:10-12), plus the output's
+  own rounding for bf16/f16 outputs (half an ulp: 2^-8 |v| for bf16).
+- int8 -> int32 bit-exact against exact integer products; the dequant epilogue bit-exact against the oracle's
+  stated order bf16((f32(acc) * sa[i]) * sb[j]).
+- Bias and ReLU/GELU against fp64 closed forms.
+- BASELINE.json's full sizes through the exact fp64 product (BLAS on the host).
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import helpers as H
+from cairn_amd import hip
+from cairn_amd import lib as L
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*what):
+    print("[gpu]", *what, flush=True)
+    sys.stdout.flush()
+
+
+def run_gemm(ab_type, c_type, m, n, k, a, b, c_init=None, *, trans_a=False, trans_b=False, accumulate=False,
+             act=L.ACT_NONE, bias=None, bias_type=L.F32, row_scale=None, col_scale=None, kernel=0, ldc=0):  # fmt: skip
+    """Upload, run one cairn_gemm_run on the null stream, synchronize, download c."""
+    out_dtype = {L.F32: np.float32, L.BF16: np.uint16, L.F16: np.uint16, L.I32: np.int32}[c_type]
+    ldc = ldc or n
+    c_host = np.zeros((m, ldc), dtype=out_dtype) if c_init is None else np.ascontiguousarray(c_init, dtype=out_dtype)
+    bufs = [hip.Buffer.of(np.ascontiguousarray(x)) if x is not None else None
+            for x in (a, b, c_host, bias, row_scale, col_scale)]  # fmt: skip
+    da, db, dc, dbias, drs, dcs = bufs
+    d = L.desc(ab_type, c_type, m, n, k, da.ptr if da else None, db.ptr if db else None, dc.ptr,
+               trans_a=trans_a, trans_b=trans_b, ldc=ldc, accumulate=accumulate, act=act,
+               bias=dbias.ptr if dbias else None, bias_type=bias_type, row_scale=drs.ptr if drs else None,
+               col_scale=dcs.ptr if dcs else None, kernel=kernel)  # fmt: skip
+    choice = L.select(d)
+    say(f"run {L.TYPE_NAMES[ab_type]}->{L.TYPE_NAMES[c_type]} {m}x{n}x{k} ta={trans_a} tb={trans_b} -> {choice['name']}")
+    L.run(d)
+    hip.synchronize()
+    out = dc.download(c_host.shape, out_dtype)
+    for x in bufs:
+        if x is not None:
+            x.close()
+    return out, choice
+
+
+# ------------------------------------------------------------------ the reference's device shapes, exact
+
+DEVICE_SHAPES = [(1, 1, 1, 1), (65, 63, 33, 2), (130, 70, 100, 3), (64, 64, 32, 4), (72, 80, 96, 5), (129, 136, 8, 6),
+                 (3, 4, 0, 7)]  # fmt: skip
+
+
+@pytest.mark.parametrize("name", list(H.FORMATS))
+def test_the_reference_device_shapes_equal_the_host_loop_bit_for_bit(name):
+    fmt = H.FORMATS[name]
+    for m, n, k, seed in DEVICE_SHAPES:
+        a = H.encode(fmt, H.device_values(m * k, seed, 2654435761)).reshape(m, k)
+        b = H.encode(fmt, H.device_values(k * n, seed * 3, 40503)).reshape(k, n)
+        c0 = (H.tile_values(m * n, 99 + seed) / 2).astype(np.float32).reshape(m, n)
+        want = c0.copy()
+        assert H.mma(fmt, m, n, k, want, a, b) == 0
+        got, _ = run_gemm(fmt, L.F32, m, n, k, a, b, c0, accumulate=True)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, m, n, k)
+
+
+def test_the_tile_simulator_shapes_equal_the_host_loop_for_every_kernel():
+    """Every tiled kernel (each layout, tile and operand size) on shapes with tails, exact data."""
+    for info in L.kernels():
+        if info["family"] != "mfma":
+            continue
+        ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
+        for m, n, k in [(8, 8, 16), (info["tile_m"] + 8, info["tile_n"] + 24, 200), (264, 136, 72)]:
+            if t == L.I8:
+                k = (k + 15) // 16 * 16
+                av = (H.tile_values(m * k, 7 + m) * 16).astype(np.int8)
+                bv = (H.tile_values(k * n, 9 + n) * 16).astype(np.int8)
+                a = (av.reshape(k, m) if ta else av.reshape(m, k))
+                b = (bv.reshape(n, k) if tb else bv.reshape(k, n))
+                got, ch = run_gemm(L.I8, L.I32, m, n, k, a, b, trans_a=ta, trans_b=tb, kernel=info["id"])
+                want = H.gemm_i8(m, n, k, a, b, trans_a=ta, trans_b=tb)
+                assert np.array_equal(got, want), (info["name"], m, n, k)
+            else:
+                a = H.encode(t, H.tile_values(m * k, 7 + m)).reshape((k, m) if ta else (m, k))
+                b = H.encode(t, H.tile_values(k * n, 9 + n)).reshape((n, k) if tb else (k, n))
+                c0 = (H.tile_values(m * n, 5) / 4).astype(np.float32).reshape(m, n)
+                got, ch = run_gemm(t, L.F32, m, n, k, a, b, c0, trans_a=ta, trans_b=tb, accumulate=True,
+                                   kernel=info["id"])  # fmt: skip
+                exact, _ = H.gemm_f64(t, m, n, k, a, b, trans_a=ta, trans_b=tb)
+                assert np.array_equal(got, (c0.astype(np.float64) + exact).astype(np.float32)), (info["name"], m, n, k)
+            assert ch["kernel"] == info["id"]
+
+
+# ------------------------------------------------------------------ random operands: the contract
+
+LAYOUTS = [(False, False), (False, True), (True, False), (True, True)]
+
+
+@pytest.mark.parametrize("trans_a,trans_b", LAYOUTS)
+@pytest.mark.parametrize("fmt", [L.BF16, L.F16])
+def test_random_operands_keep_the_contract_on_every_layout(fmt, trans_a, trans_b):
+    rng = np.random.default_rng(20261201 + 2 * trans_a + trans_b)
+    for m, n, k in [(256, 256, 128), (520, 264, 200), (72, 1032, 1000)]:
+        av = rng.normal(0, 1, (k, m) if trans_a else (m, k)).astype(np.float32)
+        bv = rng.normal(0, 1, (n, k) if trans_b else (k, n)).astype(np.float32)
+        a = H.bf16_from_f32(av) if fmt == L.BF16 else av.astype(np.float16).view(np.uint16)
+        b = H.bf16_from_f32(bv) if fmt == L.BF16 else bv.astype(np.float16).view(np.uint16)
+        A = H.values(fmt, a)
+        B = H.values(fmt, b)
+        A = A.T if trans_a else A
+        B = B.T if trans_b else B
+        exact, mag = H.exact_product(A, B)
+        c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
+        got, ch = run_gemm(fmt, L.F32, m, n, k, a, b, c0, trans_a=trans_a, trans_b=trans_b, accumulate=True)
+        assert ch["family"] == "mfma"
+        assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
+        # bf16 output: the contract plus half an ulp of the output format.
+        got16, _ = run_gemm(fmt, L.BF16, m, n, k, a, b, trans_a=trans_a, trans_b=trans_b)
+        v = H.f32_from_bf16(got16)
+        room = H.bound(k, np.zeros_like(c0), mag) + 2.0**-8 * np.abs(exact) * 1.01
+        assert H.outside(v, exact, room) == 0
+
+
+def test_two_runs_give_the_same_bits():
+    rng = np.random.default_rng(5)
+    m, n, k = 1024, 768, 2048
+    a = H.normal_bf16(rng, (m, k), 1.0)
+    b = H.normal_bf16(rng, (k, n), 1.0)
+    first, _ = run_gemm(L.BF16, L.F32, m, n, k, a, b)
+    second, _ = run_gemm(L.BF16, L.F32, m, n, k, a, b)
+    assert np.array_equal(first.view(np.uint32), second.view(np.uint32))
+
+
+# ------------------------------------------------------------------ int8
+
+
+@pytest.mark.parametrize("trans_a,trans_b", LAYOUTS)
+def test_int8_accumulators_are_bit_exact(trans_a, trans_b):
+    rng = np.random.default_rng(8 + 2 * trans_a + trans_b)
+    for m, n, k in [(200, 136, 80), (512, 520, 1024)]:
+        a = rng.integers(-127, 128, (k, m) if trans_a else (m, k), dtype=np.int8)
+        b = rng.integers(-127, 128, (n, k) if trans_b else (k, n), dtype=np.int8)
+        got, ch = run_gemm(L.I8, L.I32, m, n, k, a, b, trans_a=trans_a, trans_b=trans_b)
+        A = a.T if trans_a else a
+        B = b.T if trans_b else b
+        want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.int64)  # exact: every sum is below 2^53
+        assert np.array_equal(got.astype(np.int64), want), (m, n, k)
+
+
+def test_int8_extremes_do_not_overflow():
+    """All -128 against all -128 with k = 4096: 4096 * 16384 = 2^26, inside int32."""
+    m, n, k = 64, 64, 4096
+    a = np.full((m, k), -128, dtype=np.int8)
+    b = np.full((k, n), -128, dtype=np.int8)
+    got, _ = run_gemm(L.I8, L.I32, m, n, k, a, b)
+    assert np.all(got == 4096 * 16384)
+
+
+def test_the_dequant_epilogue_is_bit_exact():
+    rng = np.random.default_rng(44)
+    m, n, k = 384, 264, 512
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    sa = rng.uniform(1e-3, 1e-2, m).astype(np.float32)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    got, _ = run_gemm(L.I8, L.BF16, m, n, k, a, b, row_scale=sa, col_scale=sb)
+    acc = H.gemm_i8(m, n, k, a, b)
+    assert np.array_equal(got, H.dequant(acc, sa, sb))
+
+
+# ------------------------------------------------------------------ epilogues
+
+
+@pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_RELU, L.ACT_GELU])
+def test_bias_and_activation_match_the_closed_form(act):
+    rng = np.random.default_rng(3 + act)
+    m, n, k = 264, 392, 256
+    a = H.normal_bf16(rng, (m, k), 0.5)
+    b = H.normal_bf16(rng, (k, n), 0.5)
+    bias = H.normal_bf16(rng, (n,), 0.5)
+    exact, mag = H.exact_product(H.values(L.BF16, a), H.values(L.BF16, b))
+    pre = exact + H.values(L.BF16, bias)[None, :]
+    if act == L.ACT_RELU:
+        want = np.maximum(pre, 0)
+    elif act == L.ACT_GELU:
+        o = H.oracle()
+        want = np.vectorize(o.oracle_gelu)(pre)
+    else:
+        want = pre
+    got, _ = run_gemm(L.BF16, L.BF16, m, n, k, a, b, bias=bias, bias_type=L.BF16, act=act)
+    v = H.f32_from_bf16(got).astype(np.float64)
+    # The accumulator's contract error passes through the activation (slope <= 1.13 for GELU), then f32 erf's few
+    # ulps, then the bf16 output rounding.
+    room = 1.2 * H.bound(k, np.zeros(1), mag + np.abs(pre)) + 2.0**-8 * np.abs(want) * 1.01 + 1e-6
+    assert H.outside(v, want, room) == 0
+
+
+# ------------------------------------------------------------------ skinny decode shapes
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_skinny_decode_shapes_keep_the_contract(m):
+    rng = np.random.default_rng(100 + m)
+    n, k = 14336, 4096
+    a = H.normal_bf16(rng, (m, k), 1.0)
+    b = H.normal_bf16(rng, (n, k), 1.0 / 64)  # stored n x k: K-contiguous
+    got, ch = run_gemm(L.BF16, L.BF16, m, n, k, a, b, trans_b=True)
+    assert ch["family"] == "skinny"
+    exact, mag = H.exact_product(H.values(L.BF16, a), H.values(L.BF16, b).T)
+    v = H.f32_from_bf16(got)
+    room = H.bound(k, np.zeros(1), mag) + 2.0**-8 * np.abs(exact) * 1.01
+    assert H.outside(v, exact, room) == 0
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 8, 8), (3, 100, 72), (16, 33, 4104), (7, 14336, 24)])
+def test_skinny_tails_keep_the_contract(m, n, k):
+    rng = np.random.default_rng(m * n + k)
+    a = H.normal_bf16(rng, (m, k), 1.0)
+    b = H.normal_bf16(rng, (n, k), 1.0)
+    c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
+    got, ch = run_gemm(L.BF16, L.F32, m, n, k, a, b, c0, trans_b=True, accumulate=True)
+    assert ch["family"] == "skinny"
+    exact, mag = H.exact_product(H.values(L.BF16, a), H.values(L.BF16, b).T)
+    assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
+
+
+# ------------------------------------------------------------------ BASELINE.json's full sizes
+
+
+def test_bf16_4096_cubed_keeps_the_contract():
+    rng = np.random.default_rng(4096)
+    n = 4096
+    a = H.normal_bf16(rng, (n, n), 1 / 64)
+    b = H.normal_bf16(rng, (n, n), 1 / 64)
+    got, ch = run_gemm(L.BF16, L.BF16, n, n, n, a, b)
+    say("4096^3 ran on", ch["name"])
+    exact, mag = H.exact_product(H.values(L.BF16, a), H.values(L.BF16, b))
+    v = H.f32_from_bf16(got)
+    room = H.bound(n, np.zeros(1), mag) + 2.0**-8 * np.abs(exact) * 1.01
+    assert H.outside(v, exact, room) == 0
+    # BASELINE's metric: max |got - ref| / (sum |a b|) <= 1e-2.
+    assert float(np.max(np.abs(v - exact) / mag)) <= 1e-2
+
+
+def test_int8_4096_cubed_is_bit_exact():
+    rng = np.random.default_rng(8)
+    n = 4096
+    a = rng.integers(-127, 128, (n, n), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, n), dtype=np.int8)
+    got, _ = run_gemm(L.I8, L.I32, n, n, n, a, b)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(got.astype(np.float64), want)
