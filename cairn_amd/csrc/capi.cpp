@@ -14,6 +14,9 @@ using Launcher = hipError_t (*)(const Params&, hipStream_t);
 #define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
 #include "instances.inc"
 #undef CAIRN_MFMA_INSTANCE
+#define CAIRN_PIPE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
+#include "pipe_instances.inc"
+#undef CAIRN_PIPE_INSTANCE
 hipError_t cairn_generic(const Params&, hipStream_t);
 hipError_t cairn_skinny(const Params&, hipStream_t, int split);
 
@@ -22,7 +25,7 @@ namespace {
 constexpr int CUS = 256;              // gfx950: 8 XCDs of 32 CUs (MI350X, MI355X)
 constexpr int LDS_PER_CU = 160 * 1024;
 
-enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2 };
+enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2, PIPE = 3 };
 
 struct Kernel {
   Launcher run;
@@ -31,15 +34,19 @@ struct Kernel {
   bool ta, tb;
   int bm, bn;
   const char* name;
+  int stages;  // LDS stages (the tiled kernels)
 };
 
-#define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) {NAME, MFMA, OP, TA, TB, BM, BN, #NAME},
+#define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) {NAME, MFMA, OP, TA, TB, BM, BN, #NAME, 2},
+#define CAIRN_PIPE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, PIPE, OP, TA, TB, BM, BN, #NAME, STAGES},
 const Kernel TABLE[] = {
-    {nullptr, GENERIC, -1, false, false, 64, 64, "cairn_generic_64x64"},
-    {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 32, "cairn_skinny_bf16_nt"},
+    {nullptr, GENERIC, -1, false, false, 64, 64, "cairn_generic_64x64", 1},
+    {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 32, "cairn_skinny_bf16_nt", 0},
 #include "instances.inc"
+#include "pipe_instances.inc"
 };
 #undef CAIRN_MFMA_INSTANCE
+#undef CAIRN_PIPE_INSTANCE
 constexpr int COUNT = int(sizeof(TABLE) / sizeof(TABLE[0]));
 
 int op_of(int type) {
@@ -113,6 +120,27 @@ bool mfma_fits(const cairn_gemm_desc& d, const Kernel& k) {
   return a_ok && b_ok && c_ok;
 }
 
+// Can the pipelined kernel take it: 16-byte loads whole and aligned (K-major rows in chunks of 16 bytes of k; M/N-major
+// rows in chunks of 16 bytes of columns), offsets inside int32.
+bool pipe_fits(const cairn_gemm_desc& d, const Kernel& k) {
+  if(k.family != PIPE || k.op != op_of(d.ab_type) || k.ta != bool(d.trans_a) || k.tb != bool(d.trans_b)) return false;
+  const int es = element_size(d.ab_type), ce = 16 / es;
+  const std::uint64_t bk = 64 / es;
+  auto kmajor = [&](const void* p, std::uint64_t ld, int rows) {
+    return d.k % ce == 0 && ld % ce == 0 && aligned(p, 16) && std::uint64_t(rows) * ld * es < 0x7fff0000ULL;
+  };
+  auto mnmajor = [&](const void* p, std::uint64_t ld, std::uint64_t cols) {
+    return cols % ce == 0 && ld % ce == 0 && aligned(p, 16) && bk * ld * es < 0x7fff0000ULL;
+  };
+  const bool a_ok = d.trans_a ? mnmajor(d.a, d.lda, d.m) : kmajor(d.a, d.lda, k.bm);
+  const bool b_ok = d.trans_b ? kmajor(d.b, d.ldb, k.bn) : mnmajor(d.b, d.ldb, d.n);
+  const int os = output_size(d.c_type);
+  const bool c_ok = d.n % 4 == 0 && d.ldc % 4 == 0 && aligned(d.c, 4 * os);
+  return a_ok && b_ok && c_ok;
+}
+
+bool tiled_fits(const cairn_gemm_desc& d, const Kernel& k) { return k.family == PIPE ? pipe_fits(d, k) : mfma_fits(d, k); }
+
 // The skinny kernel: bf16, b stored n x k (the decode layout), m <= 16, every row 16-byte whole.
 bool skinny_fits(const cairn_gemm_desc& d) {
   return d.ab_type == CAIRN_TYPE_BF16 && !d.trans_a && d.trans_b && d.m <= 16 && d.k % 8 == 0 && d.lda % 8 == 0 &&
@@ -121,9 +149,14 @@ bool skinny_fits(const cairn_gemm_desc& d) {
 }
 
 // Workgroups of a tile shape one CU holds at once: LDS is the limit (two stages of both operands).
+int lds_bytes(const Kernel& k) {
+  if(k.family == PIPE) return k.stages * (k.bm + k.bn) * 64;
+  if(k.family == MFMA) return 2 * (k.bm + k.bn) * 128;
+  return k.family == GENERIC ? 4096 : 8192;
+}
 int resident(const Kernel& k) {
-  if(k.family != MFMA) return 8;
-  const int lds = 2 * (k.bm + k.bn) * 128;
+  if(k.family != MFMA && k.family != PIPE) return 8;
+  const int lds = lds_bytes(k);
   return std::max(1, std::min(2, LDS_PER_CU / lds));
 }
 
@@ -131,9 +164,17 @@ int resident(const Kernel& k) {
 // MFMA from LDS and L2. These are the selector's model, refit from the measured rates the benchmark records.
 double shape_rate(const Kernel& k) {
   const int area = k.bm * k.bn;
+  if(k.family == PIPE) return area >= 256 * 256 ? 2.0 : (area >= 256 * 128 ? 1.8 : 1.5);
   if(area >= 256 * 256) return 1.0;
   if(area >= 256 * 128) return 0.92;
   return 0.78;
+}
+
+// k elements a k-step of the kernel covers.
+int tile_k(const Kernel& k) {
+  const int bytes = k.family == MFMA ? 128 : (k.family == PIPE ? 64 : 32);
+  if(k.family == SKINNY) return 32;
+  return k.op == cairn::gemm::OP_I8 ? bytes : bytes / 2;
 }
 
 struct Estimate {
@@ -159,7 +200,7 @@ Estimate estimate(const cairn_gemm_desc& d, const Kernel& k) {
   // Time: rounds of resident tiles, each round a tile's k-loop at the shape's rate (resident tiles share a CU).
   e.cost = rounds * double(k.bm) * double(k.bn) * resident(k) / shape_rate(k);
   const double useful = double(d.m) * double(d.n);
-  e.efficiency = useful / (rounds * double(slots) * double(k.bm) * double(k.bn)) * shape_rate(k);
+  e.efficiency = useful / (rounds * double(slots) * double(k.bm) * double(k.bn));
   return e;
 }
 
@@ -171,7 +212,7 @@ int choose(const cairn_gemm_desc& d, int named) {
     const Kernel& k = TABLE[named - 1];
     if(k.family == GENERIC) return named;
     if(k.family == SKINNY) return skinny_fits(d) && d.c_type != CAIRN_TYPE_I32 ? named : -CAIRN_E_KERNEL;
-    return mfma_fits(d, k) ? named : -CAIRN_E_KERNEL;
+    return tiled_fits(d, k) ? named : -CAIRN_E_KERNEL;
   }
   if(d.m <= 16 && skinny_fits(d)) {
     for(int id = 1; id <= COUNT; ++id)
@@ -181,7 +222,7 @@ int choose(const cairn_gemm_desc& d, int named) {
   double cost = 0;
   for(int id = 1; id <= COUNT; ++id) {
     const Kernel& k = TABLE[id - 1];
-    if(!mfma_fits(d, k)) continue;
+    if(!tiled_fits(d, k)) continue;
     const double c = estimate(d, k).cost;
     if(!best || c < cost) best = id, cost = c;
   }
@@ -239,9 +280,9 @@ int cairn_gemm_kernel_info(int32_t id, cairn_gemm_kernel* out) {
   out->trans_b = k.tb;
   out->tile_m = k.bm;
   out->tile_n = k.bn;
-  out->tile_k = k.family == MFMA ? (k.op == cairn::gemm::OP_I8 ? 128 : 64) : (k.family == SKINNY ? 256 : 16);
-  out->threads = 256;
-  out->lds_bytes = k.family == MFMA ? 2 * (k.bm + k.bn) * 128 : (k.family == GENERIC ? 4096 : 0);
+  out->tile_k = tile_k(k);
+  out->threads = k.family == PIPE ? 512 : 256;
+  out->lds_bytes = lds_bytes(k);
   out->family = k.family;
   std::strncpy(out->name, k.name, sizeof(out->name) - 1);
   return CAIRN_OK;
@@ -272,7 +313,7 @@ int cairn_gemm_select(const cairn_gemm_desc* desc, cairn_gemm_choice* out) {
     out->family = k.family;
     out->tile_m = k.bm;
     out->tile_n = k.bn;
-    out->tile_k = k.family == MFMA ? (k.op == cairn::gemm::OP_I8 ? 128 : 64) : (k.family == SKINNY ? 256 : 16);
+    out->tile_k = tile_k(k);
     out->workgroups = e.workgroups;
     out->waves = e.waves;
     out->efficiency = e.efficiency;

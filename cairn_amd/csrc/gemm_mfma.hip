@@ -15,42 +15,11 @@
 // its gfx950 replacement, sized for 256 CUs of 160 KiB LDS and a 64-wide wave.
 #include <hip/hip_runtime.h>
 #include "kernels.hpp"
+#include "mfma.hpp"
 #include "tile.hpp"
 
 namespace cairn::gemm {
 using namespace cairn::tile;
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef int i32x16 __attribute__((ext_vector_type(16)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-template<int OP> struct Mfma;
-template<> struct Mfma<OP_BF16> {
-  using Acc = f32x16;
-  static constexpr int ES = 2;
-  __device__ static Acc step(u32x4 x, u32x4 y, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x), __builtin_bit_cast(bf16x8, y), c,
-                                                   0, 0, 0);
-  }
-};
-template<> struct Mfma<OP_F16> {
-  using Acc = f32x16;
-  static constexpr int ES = 2;
-  __device__ static Acc step(u32x4 x, u32x4 y, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x), __builtin_bit_cast(f16x8, y), c, 0,
-                                                  0, 0);
-  }
-};
-template<> struct Mfma<OP_I8> {
-  using Acc = i32x16;
-  static constexpr int ES = 1;
-  __device__ static Acc step(u32x4 x, u32x4 y, Acc c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, x), __builtin_bit_cast(i32x4, y), c, 0, 0,
-                                                 0);
-  }
-};
 
 // The device's memory policy for Operand: buffer loads, which return zero past the resource.
 struct Buffer {

@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <vector>
+#include "pipe.hpp"
 #include "tile.hpp"
 
 using namespace cairn::tile;
@@ -254,6 +255,170 @@ template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k,
     }
 }
 
+// ---------------------------------------------------------------- the pipelined kernel (gemm_pipe.hip, pipe.hpp)
+
+bool bad_read = false;
+template<int ES, int R> int frag_mn(int n0, int s, int h, int l) { return cairn::pipe::mnmajor_fragment<ES, R>(n0, s, h, l); }
+
+// The direct loads: lane `lane` of the issuing wave writes 16 bytes at the wave's LDS base + 16 lane.
+struct HostDma {
+  HostMem* mem;
+  HostLds* lds;
+  const std::uint8_t* ring;  // lds->bytes.data()
+  int lane = 0;
+  using Rsrc = HostMem::Rsrc;
+  Rsrc resource(const char* base, std::int64_t bytes) { return mem->resource(base, bytes); }
+  void load_lds(Rsrc r, char* wave_base, int offset) {
+    const u32x4 v = mem->load16(r, offset);
+    lds->write16(int(reinterpret_cast<std::uint8_t*>(wave_base) - ring) + 16 * lane, v);
+  }
+};
+
+template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad, int group) {
+  constexpr int BM = Sh::BM, BN = Sh::BN, ES = Sh::ES;
+  constexpr bool AK = !TA, BKM = TB;
+  const char* lay = TA ? (TB ? "TT" : "TN") : (TB ? "NT" : "NN");
+  const std::int64_t lda = (TA ? m : k) + pad, ldb = (TB ? k : n) + pad, ldc = n + pad;
+  const std::int64_t arows = TA ? k : m, brows = TB ? n : k;
+  const std::int64_t abytes = std::max<std::int64_t>(1, ((arows ? arows - 1 : 0) * lda + (TA ? m : k)) * ES);
+  const std::int64_t bbytes = std::max<std::int64_t>(1, ((brows ? brows - 1 : 0) * ldb + (TB ? k : n)) * ES);
+  std::vector<std::uint8_t> A(abytes, 0x7f), B(bbytes, 0x7f);
+  for(std::int64_t r = 0; r < arows; ++r)
+    for(int q = 0; q < (TA ? m : k); ++q) put<ES>(A, r * lda + q, mix(11 + r * 7919 + q));
+  for(std::int64_t r = 0; r < brows; ++r)
+    for(int q = 0; q < (TB ? k : n); ++q) put<ES>(B, r * ldb + q, mix(23 + r * 104729 + q));
+  auto a_at = [&](int i, int p) { return TA ? std::int64_t(p) * lda + i : std::int64_t(i) * lda + p; };
+  auto b_at = [&](int p, int j) { return TB ? std::int64_t(j) * ldb + p : std::int64_t(p) * ldb + j; };
+  std::vector<double> C(std::size_t(m) * ldc), old(std::size_t(m) * ldc);
+  std::vector<int> written(std::size_t(m) * ldc);
+  for(std::size_t e = 0; e < C.size(); ++e) C[e] = old[e] = double(std::int64_t(mix(99 + e) % 9) - 4) / 4.0;
+
+  const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN, total = tiles_m * tiles_n;
+  HostMem mem_a{reinterpret_cast<const char*>(A.data()), reinterpret_cast<const char*>(A.data()) + A.size()};
+  HostMem mem_b{reinterpret_cast<const char*>(B.data()), reinterpret_cast<const char*>(B.data()) + B.size()};
+  for(int wg = 0; wg < total; ++wg) {
+    int tm, tn;
+    tile_of(wg, tiles_m, tiles_n, group, tm, tn);
+    const int row0 = tm * BM, col0 = tn * BN;
+    const Panel pa = panel(AK, row0, m, k, lda, ES), pb = panel(BKM, col0, n, k, ldb, ES);
+    const char* a = reinterpret_cast<const char*>(A.data()) + pa.start;
+    const char* b = reinterpret_cast<const char*>(B.data()) + pb.start;
+    std::vector<cairn::pipe::Loader<Sh, BM, AK, HostDma>> la(256);
+    std::vector<cairn::pipe::Loader<Sh, BN, BKM, HostDma>> lb(256);
+    for(int gt = 0; gt < 256; ++gt) {
+      la[gt].setup(gt, row0, m, lda);
+      lb[gt].setup(gt, col0, n, ldb);
+    }
+    std::vector<double> acc(static_cast<std::size_t>(BM * BN), 0.0);
+    const int T = (k + Sh::BK - 1) / Sh::BK;
+    for(int st = 0; st < T; ++st) {
+      HostLds lds(Sh::STAGE);  // one stage of the ring (the ring's other stages are the same code at other bases)
+      HostDma da{&mem_a, &lds, lds.bytes.data()}, db{&mem_b, &lds, lds.bytes.data()};
+      for(int gt = 0; gt < 256; ++gt) {
+        da.lane = db.lane = gt & 63;
+        la[gt].issue(da, a, pa.bytes, lda, st, k, reinterpret_cast<char*>(lds.bytes.data()), gt >> 6);
+        lb[gt].issue(db, b, pb.bytes, ldb, st, k, reinterpret_cast<char*>(lds.bytes.data()) + Sh::A_BYTES, gt >> 6);
+      }
+      if(mem_a.bad || mem_b.bad) FAIL("pipe %s %dx%d es=%d %dx%dx%d: a global load outside its matrix", lay, BM, BN, ES, m, n, k);
+      if(lds.bad) FAIL("pipe %s: an LDS write off the stage", lay);
+      for(int c = 0; c < Sh::STAGE / 16; ++c)
+        if(lds.writes[c] != 1) FAIL("pipe %s %dx%d es=%d: LDS chunk %d written %d times", lay, BM, BN, ES, c, lds.writes[c]);
+      for(int wave = 0; wave < 8; ++wave) {
+        const int grp = wave >> 2, w4 = wave & 3;
+        for(int s = 0; s < 2; ++s)
+          for(int i = 0; i < Sh::FM; ++i)
+            for(int j = 0; j < Sh::FN; ++j) {
+              std::uint8_t fa[64][16], fb[64][16];
+              auto gather = [&](bool kmajor, int base, int R, int row0_, std::uint8_t (&out)[64][16]) {
+                if(kmajor) {
+                  for(int l = 0; l < 64; ++l) {
+                    const int at = base + cairn::pipe::kmajor_fragment(row0_, s, l);
+                    if(at < base || at + 16 > base + R * 64) bad_read = true;
+                    std::memcpy(out[l], &lds.bytes[at], 16);
+                  }
+                } else {
+                  for(int h = 0; h < 2; ++h) {
+                    int addr[64];
+                    for(int l = 0; l < 64; ++l) {
+                      addr[l] = base + (R == BM ? frag_mn<ES, BM>(row0_, s, h, l) : frag_mn<ES, BN>(row0_, s, h, l));
+                      if(addr[l] < base || addr[l] + 8 > base + R * 64) bad_read = true;
+                    }
+                    std::uint8_t got[64][8];
+                    cairn::pipe::transpose_read(lds.bytes.data(), addr, ES, got);
+                    for(int l = 0; l < 64; ++l) std::memcpy(out[l] + 8 * h, got[l], 8);
+                  }
+                }
+              };
+              gather(AK, 0, BM, grp * Sh::WTM + 32 * i, fa);
+              gather(BKM, Sh::A_BYTES, BN, w4 * Sh::WTN + 32 * j, fb);
+              if(bad_read) FAIL("pipe %s: a fragment read off its operand's stage", lay);
+              double P[32][32], Q[32][32];
+              constexpr int CE = 16 / ES;
+              for(int l = 0; l < 64; ++l) {
+                double pv[16], qv[16];
+                decode<ES>(fb[l], pv);
+                decode<ES>(fa[l], qv);
+                for(int e = 0; e < CE; ++e) {
+                  P[l & 31][(l >> 5) * CE + e] = pv[e];
+                  Q[(l >> 5) * CE + e][l & 31] = qv[e];
+                }
+              }
+              for(int l = 0; l < 64; ++l)
+                for(int r = 0; r < 16; ++r) {
+                  const int prow = 8 * (r / 4) + 4 * (l / 32) + r % 4, qcol = l % 32;
+                  double sum = 0;
+                  for(int kk = 0; kk < 2 * CE; ++kk) sum += P[prow][kk] * Q[kk][qcol];
+                  const int mm = grp * Sh::WTM + 32 * i + acc_m(l);
+                  const int nn = w4 * Sh::WTN + 32 * j + acc_n(l, r / 4) + r % 4;
+                  acc[std::size_t(mm) * BN + nn] += sum;
+                }
+            }
+      }
+    }
+    for(int wave = 0; wave < 8; ++wave) {
+      const int grp = wave >> 2, w4 = wave & 3;
+      for(int i = 0; i < Sh::FM; ++i)
+        for(int j = 0; j < Sh::FN; ++j)
+          for(int l = 0; l < 64; ++l)
+            for(int q = 0; q < 4; ++q) {
+              const int mm = grp * Sh::WTM + 32 * i + acc_m(l), nn0 = w4 * Sh::WTN + 32 * j + acc_n(l, q);
+              const int gm = row0 + mm, gn = col0 + nn0;
+              if(gm >= m || gn >= n) continue;
+              for(int e = 0; e < 4; ++e) {
+                const std::size_t at = std::size_t(gm) * ldc + gn + e;
+                C[at] = old[at] + acc[std::size_t(mm) * BN + nn0 + e];
+                ++written[at];
+              }
+            }
+    }
+  }
+  for(int i = 0; i < m; ++i)
+    for(int j = 0; j < n; ++j) {
+      double exact = 0;
+      for(int p = 0; p < k; ++p) exact += value_of<ES>(A, a_at(i, p)) * value_of<ES>(B, b_at(p, j));
+      const std::size_t at = std::size_t(i) * ldc + j;
+      if(written[at] != 1) FAIL("pipe %s %dx%d es=%d %dx%dx%d: output (%d,%d) written %d times", lay, BM, BN, ES, m, n, k, i, j, written[at]);
+      if(C[at] != old[at] + exact)
+        FAIL("pipe %s %dx%d es=%d %dx%dx%d pad %d: output (%d,%d) is %.9g, exact %.9g", lay, BM, BN, ES, m, n, k, pad, i,
+             j, C[at], old[at] + exact);
+    }
+}
+
+template<class Sh> void pipe_shapes() {
+  constexpr int CE = 16 / Sh::ES, MN = Sh::ES == 2 ? 8 : 16;  // k chunk; m, n pieces of an M/N-major row
+  const int list[][5] = {{MN, MN, CE, 0, 4},
+                         {Sh::BM, Sh::BN, 64 / Sh::ES, 0, 4},
+                         {Sh::BM + MN, Sh::BN + 2 * MN, 3 * CE, 16, 1},
+                         {2 * Sh::BM + 4 * MN, Sh::BN - MN, 200 / CE * CE, 16, 2},
+                         {264 / MN * MN, Sh::BN + MN, 37 * CE, 0, 4}};
+  for(auto& s : list) {
+    run_pipe<Sh, false, false>(s[0], s[1], s[2], s[3], s[4]);
+    run_pipe<Sh, false, true>(s[0], s[1], s[2], s[3], s[4]);
+    run_pipe<Sh, true, false>(s[0], s[1], s[2], s[3], s[4]);
+    run_pipe<Sh, true, true>(s[0], s[1], s[2], s[3], s[4]);
+  }
+}
+
 template<int BM, int BN, int ES> void layouts(int m, int n, int k, int pad, int group) {
   run<BM, BN, ES, false, false>(m, n, k, pad, group);
   run<BM, BN, ES, false, true>(m, n, k, pad, group);
@@ -274,6 +439,16 @@ template<int BM, int BN, int ES> void shapes() {
 }  // namespace
 
 int main() {
+  pipe_shapes<cairn::pipe::Shape<256, 256, 2, 4>>();
+  pipe_shapes<cairn::pipe::Shape<256, 256, 1, 4>>();
+  pipe_shapes<cairn::pipe::Shape<256, 128, 2, 4>>();
+  pipe_shapes<cairn::pipe::Shape<128, 256, 2, 4>>();
+  pipe_shapes<cairn::pipe::Shape<128, 128, 2, 4>>();
+  pipe_shapes<cairn::pipe::Shape<128, 128, 1, 4>>();
+  if(failures) {
+    std::printf("pipe: %d failures\n", failures);
+    return 1;
+  }
   shapes<256, 256, 2>();
   shapes<256, 128, 2>();
   shapes<128, 256, 2>();
