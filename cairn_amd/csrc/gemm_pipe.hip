@@ -25,8 +25,14 @@
 
 namespace cairn::gemm {
 using namespace cairn::pipe;
+typedef unsigned su32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// The LDS address of a pointer into the workgroup's LDS.
+__device__ inline unsigned lds_address(const char* p) {
+  return unsigned(reinterpret_cast<std::uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 __device__ inline __amdgpu_buffer_rsrc_t span_of(const char* base, std::int64_t bytes) {
@@ -34,38 +40,52 @@ __device__ inline __amdgpu_buffer_rsrc_t span_of(const char* base, std::int64_t 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)capped, 0x00020000);
 }
 
-// The device's policy for Loader: a buffer resource, and one 16-byte load per lane into LDS at the wave's base +
-// 16 lane (the lane's own offset chooses what it fetches).
+// The device's policy for Loader: a buffer resource (four SGPRs), and one 16-byte load per lane into LDS at the
+// wave's base + 16 lane (the lane's own offset chooses what it fetches). The load is written out here, M0 set from a
+// scalar, so that the compiler does not see LDS written behind its back and wait on every prefetch in flight before
+// the LDS reads of a stage that has long landed; the kernel orders the prefetches itself (vmcnt waits and barriers).
 struct Dma {
-  using Rsrc = __amdgpu_buffer_rsrc_t;
-  __device__ static Rsrc resource(const char* base, std::int64_t bytes) { return span_of(base, bytes); }
+  using Rsrc = su32x4;
+  __device__ static Rsrc resource(const char* base, std::int64_t bytes) {
+    const std::int64_t capped = bytes < 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffffLL : bytes);
+    const std::uint64_t addr = reinterpret_cast<std::uintptr_t>(base);
+    return Rsrc{unsigned(addr), unsigned(addr >> 32) & 0xffffu, unsigned(capped), 0x00020000u};
+  }
   __device__ static void load_lds(Rsrc r, char* wave_base, int offset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(wave_base), 16, offset, 0, 0, 0);
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_address(wave_base));
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(offset), "s"(r)
+                 : "memory", "m0");
   }
 };
 
 // Wait until at most N of this wave's vector-memory operations are outstanding, then (barrier) until every wave
 // of the workgroup has reached the same point with its LDS reads complete.
 template<int N> __device__ inline void wait_loads() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
-__device__ inline void barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ inline void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// An MFMA operand of lane l for the 32-row block at `row0` of an operand held R rows wide, k-step s.
-template<class Sh, int R, bool KMAJOR> __device__ inline u32x4 fragment(const char* stage, int row0, int s, int l) {
+// The MFMA operands of one k-step s for COUNT 32-row blocks at row0 + 32 i of an operand held R rows wide: K-major,
+// one ds_read_b128 each; M/N-major, two transpose reads each (k bytes 0-7, then 8-15 of the lane's 16).
+template<class Sh, int R, bool KMAJOR, int COUNT>
+__device__ inline void fragments(u32x4 (&out)[COUNT], const char* stage, int row0, int s, int l) {
   if constexpr(KMAJOR) {
-    return *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(row0, s, l));
-  } else if constexpr(Sh::ES == 2) {
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(stage + mnmajor_fragment<2, R>(row0, s, 0, l)));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(stage + mnmajor_fragment<2, R>(row0, s, 1, l)));
-    const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
-    return u32x4{a[0], a[1], b[0], b[1]};
+#pragma unroll
+    for(int i = 0; i < COUNT; ++i) out[i] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(row0 + 32 * i, s, l));
   } else {
-    const i32x2 lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-        (__attribute__((address_space(3))) i32x2*)(stage + mnmajor_fragment<1, R>(row0, s, 0, l)));
-    const i32x2 hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-        (__attribute__((address_space(3))) i32x2*)(stage + mnmajor_fragment<1, R>(row0, s, 1, l)));
-    return u32x4{std::uint32_t(lo[0]), std::uint32_t(lo[1]), std::uint32_t(hi[0]), std::uint32_t(hi[1])};
+#pragma unroll
+    for(int i = 0; i < COUNT; ++i) {
+      u32x2 half[2];
+#pragma unroll
+      for(int h = 0; h < 2; ++h) {
+        const char* at = stage + mnmajor_fragment<Sh::ES, R>(row0 + 32 * i, s, h, l);
+        if constexpr(Sh::ES == 2)
+          half[h] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                  (__attribute__((address_space(3))) s16x4*)(at)));
+        else
+          half[h] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                                                  (__attribute__((address_space(3))) i32x2*)(at)));
+      }
+      out[i] = u32x4{half[0][0], half[0][1], half[1][0], half[1][1]};
+    }
   }
 }
 
@@ -77,7 +97,8 @@ __global__ void __launch_bounds__(512) pipe_gemm(Params p) {
   constexpr int S = Sh::STAGES;
   __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, group = wave >> 2, w4 = wave & 3, gt = t & 255;
+  const int t = threadIdx.x, lane = t & 63, gt = t & 255;
+  const int wave = t >> 6, group = wave >> 2, w4 = wave & 3;
   int tm, tn;
   cairn::tile::tile_of(int(blockIdx.x), p.tiles_m, p.tiles_n, p.group, tm, tn);
   const int row0 = tm * Sh::BM, col0 = tn * Sh::BN;
@@ -119,17 +140,15 @@ __global__ void __launch_bounds__(512) pipe_gemm(Params p) {
     for(int j = 0; j < Sh::FN; ++j) acc[i][j] = Acc{};
   u32x4 xa[2][Sh::FM], xb[2][Sh::FN];
 
+  // A group's fragment reads of stage st. No wait follows them: the group's next phase is its MFMAs, which wait for
+  // their own operands, and a stage's buffer is refilled only in a phase B after both groups' MFMAs of that stage.
   auto memory = [&](int st) {
     const char* stage = lds + (st % S) * Sh::STAGE;
 #pragma unroll
     for(int s = 0; s < 2; ++s) {
-#pragma unroll
-      for(int i = 0; i < Sh::FM; ++i) xa[s][i] = fragment<Sh, Sh::BM, AK>(stage, group * Sh::WTM + 32 * i, s, lane);
-#pragma unroll
-      for(int j = 0; j < Sh::FN; ++j)
-        xb[s][j] = fragment<Sh, Sh::BN, BKM>(stage + Sh::A_BYTES, w4 * Sh::WTN + 32 * j, s, lane);
+      fragments<Sh, Sh::BM, AK, Sh::FM>(xa[s], stage, group * Sh::WTM, s, lane);
+      fragments<Sh, Sh::BN, BKM, Sh::FN>(xb[s], stage + Sh::A_BYTES, w4 * Sh::WTN, s, lane);
     }
-    if(st + S - 1 < T) issue(st + S - 1);
   };
   auto compute = [&]() {
 #pragma unroll
@@ -156,6 +175,9 @@ __global__ void __launch_bounds__(512) pipe_gemm(Params p) {
     } else if(it < T) {
       memory(it);
     }
+    // Both groups refill stage it - 1's buffer with stage it + S - 1: group 0 computed stage it - 1 in the previous
+    // phase B, group 1 in the phase A just ended.
+    if(it < T && it + S - 1 < T) issue(it + S - 1);
     if(it + 1 < T) landed(it + 1, (it + S - 1 < T - 1 ? it + S - 1 : T - 1));
     barrier();
   }

@@ -6,15 +6,19 @@
 // 64 bytes of every row's k per stage (32 bf16/f16 or 64 int8: two MFMA k-steps). Each operand keeps the layout it
 // has in memory:
 //
-//  - K-major (a of NN/NT, b of NT/TT): R rows of 64 bytes, chunk c of row r at physical chunk c ^ ((r >> 1) & 3);
+//  - K-major (a of NN/NT, b of NT/TT): R rows of 64 bytes, chunk c of row r at physical chunk c ^ ((r >> 2) & 3);
 //    an MFMA operand is one ds_read_b128 per lane.
-//  - M/N-major (b of NN, a of TN/TT): k rows of R elements, chunk c of k row kk at physical chunk
-//    c ^ (2 (kk & 3)) for 16-bit elements (a row is R / 8 chunks) or c ^ (kk & 7) for bytes (R / 16 chunks); an MFMA
-//    operand is two LDS transpose reads per lane (ds_read_b64_tr_b16 / tr_b8), which hand each lane one column of a
-//    4 x 16 (16-bit) or 8 x 16 (byte) block that 16 lanes read row-wise.
+//  - M/N-major (b of NN, a of TN/TT): k rows of R elements, chunk c of k row kk at physical chunk c ^ swz(kk):
+//    4 (kk & 3) for 16-bit elements, 2 (kk & 7) for bytes (2 ((kk >> 1) & 3) where a row is only 128 bytes); an
+//    MFMA operand is two LDS transpose reads per lane (ds_read_b64_tr_b16 / tr_b8), which hand each lane one column
+//    of a 4 x 16 (16-bit) or 8 x 16 (byte) block that 16 lanes read row-wise.
 //
-// The swizzles put the eight 16-byte chunks a group of eight lanes reads, and the four (eight) rows a transpose read
-// touches, on distinct banks. Both operand kinds give lane l the same k for the same register byte: lane l holds
+// gfx950's LDS serves 64 banks of 4 bytes a clock: a ds_read_b128 in phases of 16 lanes, a 64-bit (transpose) read in
+// phases of 32. The swizzles give every phase distinct banks: the 16 rows a b128 phase reads at one chunk fall on the
+// four 64-byte quarters of a bank row and four chunk positions in each; the two 16-lane groups of a transpose phase
+// read 4 (8) rows by 32 (16) adjacent bytes each, spread over the 16 chunk positions of a bank row. Measured as zero
+// bank-conflict cycles (SQ_LDS_BANK_CONFLICT). Both operand kinds give lane l the same k for the same register
+// byte: lane l holds
 // k = 32 s + 16 (l / 32) + (byte of its 16), in bytes, for MFMA k-step s of the stage. So the pairing of a and b
 // along k never depends on the layouts.
 #pragma once
@@ -44,14 +48,19 @@ template<int BM_, int BN_, int ES_, int STAGES_> struct Shape {
 CAIRN_HD int slot(int t, int u) { return (u * 4 + (t >> 6)) * 64 + (t & 63); }
 
 // K-major: byte of (row r, chunk c), and the (row, chunk) slot q holds.
-CAIRN_HD int kmajor_at(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 1) & 3)); }
+CAIRN_HD int kmajor_at(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
 CAIRN_HD void kmajor_slot(int q, int& r, int& c) {
   r = q >> 2;
-  c = (q & 3) ^ ((r >> 1) & 3);
+  c = (q & 3) ^ ((r >> 2) & 3);
 }
 
 // M/N-major with R elements a k row: byte of (k row kk, chunk c), and the (k row, chunk) slot q holds.
-template<int ES, int R> CAIRN_HD int swz(int kk) { return ES == 2 ? 2 * (kk & 3) : (kk & 7); }
+template<int ES, int R> CAIRN_HD int swz(int kk) {
+  static_assert(R * ES >= 128, "an M/N-major k row is at least 128 bytes");
+  if constexpr(ES == 2) return 4 * (kk & 3);
+  else if constexpr(R >= 256) return 2 * (kk & 7);
+  else return 2 * ((kk >> 1) & 3);
+}
 template<int ES, int R> CAIRN_HD int mnmajor_at(int kk, int c) { return kk * R * ES + 16 * (c ^ swz<ES, R>(kk)); }
 template<int ES, int R> CAIRN_HD void mnmajor_slot(int q, int& kk, int& c) {
   constexpr int per = R * ES / 16;  // chunks a k row

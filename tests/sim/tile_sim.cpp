@@ -258,6 +258,19 @@ template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k,
 // ---------------------------------------------------------------- the pipelined kernel (gemm_pipe.hip, pipe.hpp)
 
 bool bad_read = false;
+bool conflict = false;
+// gfx950 LDS: 64 banks of 4 bytes. A ds_read_b128 is served 16 lanes a clock, a 64-bit read 32 lanes a clock; a
+// phase without conflicts touches each bank once.
+void check_banks(const int addr[64], int bytes) {
+  const int lanes = 256 / bytes;
+  for(int p0 = 0; p0 < 64; p0 += lanes) {
+    int seen[64] = {};
+    for(int l = p0; l < p0 + lanes; ++l)
+      for(int w = 0; w < bytes / 4; ++w) ++seen[(addr[l] / 4 + w) % 64];
+    for(int b = 0; b < 64; ++b)
+      if(seen[b] != 1) conflict = true;
+  }
+}
 template<int ES, int R> int frag_mn(int n0, int s, int h, int l) { return cairn::pipe::mnmajor_fragment<ES, R>(n0, s, h, l); }
 
 // The direct loads: lane `lane` of the issuing wave writes 16 bytes at the wave's LDS base + 16 lane.
@@ -331,11 +344,14 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
               std::uint8_t fa[64][16], fb[64][16];
               auto gather = [&](bool kmajor, int base, int R, int row0_, std::uint8_t (&out)[64][16]) {
                 if(kmajor) {
+                  int addr[64];
                   for(int l = 0; l < 64; ++l) {
                     const int at = base + cairn::pipe::kmajor_fragment(row0_, s, l);
+                    addr[l] = at;
                     if(at < base || at + 16 > base + R * 64) bad_read = true;
                     std::memcpy(out[l], &lds.bytes[at], 16);
                   }
+                  check_banks(addr, 16);
                 } else {
                   for(int h = 0; h < 2; ++h) {
                     int addr[64];
@@ -343,6 +359,7 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
                       addr[l] = base + (R == BM ? frag_mn<ES, BM>(row0_, s, h, l) : frag_mn<ES, BN>(row0_, s, h, l));
                       if(addr[l] < base || addr[l] + 8 > base + R * 64) bad_read = true;
                     }
+                    check_banks(addr, 8);
                     std::uint8_t got[64][8];
                     cairn::pipe::transpose_read(lds.bytes.data(), addr, ES, got);
                     for(int l = 0; l < 64; ++l) std::memcpy(out[l] + 8 * h, got[l], 8);
@@ -352,6 +369,7 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
               gather(AK, 0, BM, grp * Sh::WTM + 32 * i, fa);
               gather(BKM, Sh::A_BYTES, BN, w4 * Sh::WTN + 32 * j, fb);
               if(bad_read) FAIL("pipe %s: a fragment read off its operand's stage", lay);
+              if(conflict) FAIL("pipe %s %dx%d es=%d: a fragment read phase has an LDS bank conflict", lay, BM, BN, ES);
               double P[32][32], Q[32][32];
               constexpr int CE = 16 / ES;
               for(int l = 0; l < 64; ++l) {

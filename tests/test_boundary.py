@@ -1,0 +1,208 @@
+"""The drop-in boundary on the CPU: libcairn_gemm_gfx950.so loads and exports every symbol include/cairn_gemm.h
+declares, its structs have the layout the header states, the host entries (cf_mma_<fmt>: the reference loop) equal
+the oracle bit for bit, the checked entries abort where the reference traps, and the selector answers for every
+BASELINE config and refuses what no kernel computes. No test here launches GPU work.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import helpers as H
+from cairn_amd import lib as L
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "cairn_gemm.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = set(re.findall(r"^(?:[A-Za-z_][\w\s\*]*?)\b([A-Za-z_]\w*)\s*\([^;]*\)\s*;", text, flags=re.M))
+    return {n for n in names if n not in {"typedef"}}
+
+
+def test_the_library_exports_every_declared_symbol():
+    L.load()
+    names = declared_functions()
+    assert {"cairn_gemm_run", "cairn_gemm_select", "cf_mma_bf16", "cq_mma_bf16_device", "cairn_gemm_device_stream"} <= names
+    dynamic = subprocess.run(["nm", "-D", "--defined-only", str(L.LIBRARY)], capture_output=True, text=True,
+                             check=True).stdout  # fmt: skip
+    exported = {line.split()[-1] for line in dynamic.splitlines() if len(line.split()) >= 3}
+    missing = (names | set(L.DATA_SYMBOLS)) - exported
+    assert not missing, missing
+    assert names == set(L.SIGNATURES), names ^ set(L.SIGNATURES)  # the bindings type every entry
+    lib = L.load()
+    assert C.c_char_p.in_dll(lib, "cairn_interface_gemm_gfx950_1") is not None
+
+
+def test_the_structs_have_the_layout_the_header_states(tmp_path):
+    fields = {"cairn_gemm_desc": [f for f, _ in L.Desc._fields_], "cairn_gemm_kernel": [f for f, _ in L.Kernel._fields_],
+              "cairn_gemm_choice": [f for f, _ in L.Choice._fields_]}  # fmt: skip
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
+    for struct, names in fields.items():
+        lines.append(f'printf("{struct} %zu\\n", sizeof({struct}));')
+        lines += [f'printf("{struct}.{f} %zu\\n", offsetof({struct}, {f}));' for f in names]
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                              check=True).stdout.splitlines())  # fmt: skip
+    for struct, cls in (("cairn_gemm_desc", L.Desc), ("cairn_gemm_kernel", L.Kernel), ("cairn_gemm_choice", L.Choice)):
+        assert int(got[struct]) == C.sizeof(cls), struct
+        for f in fields[struct]:
+            assert int(got[f"{struct}.{f}"]) == getattr(cls, f).offset, (struct, f)
+
+
+@pytest.mark.parametrize("name", ["f32", "f16", "bf16", "f8e4m3", "f8e5m2"])
+def test_the_host_entries_are_the_reference_loop(name):
+    fmt = {"f32": H.F32, "f16": H.F16, "bf16": H.BF16, "f8e4m3": H.F8E4M3, "f8e5m2": H.F8E5M2}[name]
+    rng = np.random.default_rng(17)
+    f = getattr(L.load(), f"cf_mma_{name}")
+    for m, n, k in [(1, 1, 1), (17, 3, 33), (12, 13, 64), (40, 41, 7), (3, 4, 0)]:
+        if fmt == H.F32:
+            a = rng.uniform(-1, 1, m * k).astype(np.float32)
+            b = rng.uniform(-1, 1, k * n).astype(np.float32)
+        else:
+            a = H.encode(fmt, np.round(rng.uniform(-8, 8, m * k) * 8) / 8)
+            b = H.encode(fmt, np.round(rng.uniform(-8, 8, k * n) * 8) / 8)
+        c = rng.uniform(-4, 4, m * n).astype(np.float32)
+        want = c.copy()
+        assert H.mma(fmt, m, n, k, want, a, b) == 0
+        got = c.copy()
+        f(m, n, k, got.size, got.ctypes.data, a.size, a.ctypes.data, b.size, b.ctypes.data)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, m, n, k)
+
+
+ABORT = """
+import ctypes as C, numpy as np, sys
+sys.path.insert(0, {root!r})
+from cairn_amd import lib as L
+f = L.load().cf_mma_bf16
+a = np.zeros(6, np.uint16); b = np.zeros(9, np.uint16); c = np.zeros(6, np.float32)
+{call}
+print("returned")
+"""
+
+
+@pytest.mark.parametrize("call", [
+    "f(2, 3, 3, 6, c.ctypes.data, 6, a.ctypes.data, 6, b.ctypes.data)",   # b holds 9, the call says 6
+    "f(2, 3, 3, 5, c.ctypes.data, 6, a.ctypes.data, 9, b.ctypes.data)",   # c holds 6, the call says 5
+    "f(2, 3, 3, 6, c.ctypes.data, 6, c.ctypes.data, 9, b.ctypes.data)",   # a overlaps the read-write c
+    "f(2, 3, 3, 6, None, 6, a.ctypes.data, 9, b.ctypes.data)",            # a null view of 6 elements
+])  # fmt: skip
+def test_the_checked_entry_aborts_where_the_reference_traps(call):
+    """src/cairn/runtime/cairn_tensor.hpp:22-24 (shape), codegen.py:500-512 (views, disjoint): a failed check is
+    std::abort, SIGABRT, never a return (tests/soundness/test_tensor.py:109-119)."""
+    done = subprocess.run([sys.executable, "-c", ABORT.format(root=str(ROOT), call=call)], capture_output=True,
+                          text=True, timeout=120)  # fmt: skip
+    assert done.returncode == -6, (done.returncode, done.stdout, done.stderr[-500:])
+    assert "returned" not in done.stdout
+
+
+def test_a_and_b_may_be_one_array():
+    """test_tensor.py:105-106: a square of one matrix reads it twice."""
+    f = L.load().cf_mma_bf16
+    a = H.encode(H.BF16, np.arange(9, dtype=np.float64) / 8)
+    c = np.zeros(9, np.float32)
+    f(3, 3, 3, 9, c.ctypes.data, 9, a.ctypes.data, 9, a.ctypes.data)
+    want = np.zeros(9, np.float32)
+    H.mma(H.BF16, 3, 3, 3, want, a, a)
+    assert np.array_equal(c, want)
+
+
+# ------------------------------------------------------------------ the selector
+
+
+P = 1 << 20  # an aligned stand-in address: select only reads pointer alignment
+
+
+def choose(*args, **kw):
+    return L.select(L.desc(*args, **kw))
+
+
+def test_the_selector_picks_a_kernel_for_every_baseline_config():
+    c2 = choose(L.BF16, L.BF16, 4096, 4096, 4096, P, P, P)
+    assert c2["family"] == "pipe" and (c2["tile_m"], c2["tile_n"]) == (256, 256) and c2["workgroups"] == 256
+    c4 = choose(L.I8, L.BF16, 4096, 4096, 4096, P, P, P, row_scale=P, col_scale=P)
+    assert c4["family"] == "pipe" and "i8" in c4["name"]
+    assert choose(L.I8, L.I32, 4096, 4096, 4096, P, P, P)["family"] == "pipe"
+    for m in (1, 4, 16):
+        assert choose(L.BF16, L.BF16, m, 14336, 4096, P, P, P, trans_b=True)["family"] == "skinny"
+    fwd = choose(L.BF16, L.BF16, 8192, 11008, 4096, P, P, P, bias=P, bias_type=L.BF16, act=L.ACT_GELU)
+    dx = choose(L.BF16, L.BF16, 8192, 4096, 11008, P, P, P, trans_b=True)
+    dw = choose(L.BF16, L.BF16, 4096, 11008, 8192, P, P, P, trans_a=True)
+    assert [x["name"].split("_")[3] for x in (fwd, dx, dw)] == ["nn", "nt", "tn"]
+    assert fwd["waves"] == pytest.approx(1376 / 256) and dx["workgroups"] == 512
+
+
+def test_the_selector_falls_back_to_the_generic_kernel_where_chunks_do_not_fit():
+    assert choose(L.BF16, L.F32, 65, 63, 33, P, P, P, accumulate=True)["family"] == "generic"  # k % 8
+    assert choose(L.F8E4M3, L.F32, 256, 256, 256, P, P, P, accumulate=True)["family"] == "generic"
+    assert choose(L.BF16, L.F32, 256, 256, 256, P + 2, P, P)["family"] == "generic"  # a off 16 bytes
+    assert choose(L.BF16, L.F32, 256, 250, 256, P, P, P)["family"] == "generic"  # n % 4
+
+
+def test_the_selector_refuses_what_no_kernel_computes():
+    def status(**kw):
+        base = dict(ab_type=L.BF16, c_type=L.F32, m=64, n=64, k=64, a=P, b=P, c=P)
+        base.update(kw)
+        d = L.desc(base.pop("ab_type"), base.pop("c_type"), base.pop("m"), base.pop("n"), base.pop("k"),
+                   base.pop("a"), base.pop("b"), base.pop("c"), **base)  # fmt: skip
+        return L.load().cairn_gemm_select(C.byref(d), None)
+    assert status() == L.OK
+    assert status(c_type=L.I32) == L.E_TYPE  # int32 output is for int8 operands
+    assert status(c_type=L.BF16, accumulate=True) == L.E_TYPE  # accumulate adds into f32
+    assert status(ab_type=L.I8, c_type=L.I32, act=L.ACT_RELU) == L.E_TYPE  # the accumulator itself, no epilogue
+    assert status(lda=63) == L.E_SHAPE  # a row of 64 needs lda >= 64
+    assert status(kernel=9999) == L.E_KERNEL
+    assert status(k=60, kernel=L.kernel_named("cairn_pipe_bf16_nn_256x256")) == L.E_KERNEL  # k % 8
+    assert status(c=None) == L.E_ARG
+    assert status(act=7) == L.E_ARG
+    bad = L.desc(L.BF16, L.F32, 64, 64, 64, P, P, P)
+    bad.version = 2
+    assert L.load().cairn_gemm_select(C.byref(bad), None) == L.E_ARG
+    assert status(m=0, c=None) == L.OK  # nothing to do needs no pointers
+
+
+def test_the_kernel_table_is_consistent():
+    ks = L.kernels()
+    assert len({k["name"] for k in ks}) == len(ks)
+    for k in ks:
+        assert k["lds_bytes"] <= 160 * 1024, k
+        assert k["family"] in ("mfma", "pipe", "generic", "skinny")
+        if k["family"] == "pipe":
+            assert k["threads"] == 512 and k["tile_k"] in (32, 64)
+
+
+# ------------------------------------------------------------------ the product never leans on the oracle
+
+
+def test_the_product_does_not_reach_the_oracle():
+    for path in [*(ROOT / "cairn_amd").rglob("*.py"), *(ROOT / "cairn_amd").rglob("*.hip"),
+                 *(ROOT / "cairn_amd").rglob("*.cpp"), *(ROOT / "cairn_amd").rglob("*.hpp"), *(ROOT / "include").rglob("*.h*")]:  # fmt: skip
+        text = path.read_text()
+        assert "liboracle" not in text and "oracle_" not in text and "libcairnref" not in text, path
+
+
+def test_a_missing_library_fails_loudly(tmp_path):
+    code = f"""
+import sys; sys.path.insert(0, {str(ROOT)!r})
+from cairn_amd import lib as L
+from pathlib import Path
+L.LIBRARY = Path({str(tmp_path / 'absent.so')!r})
+try:
+    L.load()
+except L.LibraryMissing as e:
+    print("missing:", e)
+"""
+    done = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert "missing:" in done.stdout, done.stdout + done.stderr
