@@ -1,0 +1,76 @@
+"""The C++ surface in include/cairn, built with g++ on the host (tests/cpp/surface.cpp) under a recording machine:
+the execution context's rules, its traps, and the storage floats and host multiply bit for bit against the
+reference's own outputs (tests/golden/reference.npz)."""
+
+from __future__ import annotations
+
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLDEN = np.load(ROOT / "tests" / "golden" / "reference.npz")
+FORMATS = ["f16", "bf16", "f8e4m3", "f8e5m2"]
+
+
+@pytest.fixture(scope="module")
+def surface(tmp_path_factory) -> Path:
+    exe = tmp_path_factory.mktemp("surface") / "surface"
+    subprocess.run(["g++", "-std=c++20", "-O1", "-ffp-contract=off", "-Wall", "-Wextra", "-Werror",
+                    f"-I{ROOT / 'include'}", str(ROOT / "tests" / "cpp" / "surface.cpp"), "-o", str(exe)],
+                   check=True)  # fmt: skip
+    return exe
+
+
+def run(exe: Path, *args: str) -> subprocess.CompletedProcess:
+    return subprocess.run([str(exe), *args], capture_output=True, text=True, timeout=60)
+
+
+def test_the_context_keeps_the_reference_rules(surface):
+    done = run(surface, "context")
+    assert done.returncode == 0, done.stdout + done.stderr
+    lines = done.stdout.splitlines()
+    assert lines[-1] == "0 failures" and sum(line.startswith("ok ") for line in lines) >= 17
+
+
+@pytest.mark.parametrize("case", ["shape", "nested", "settle", "observe", "leaked", "overflow", "e4m3", "scale"])
+def test_misuse_traps(surface, case):
+    done = run(surface, "trap", case)
+    assert done.returncode == -6 and "returned" not in done.stdout, (done.returncode, done.stdout)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_storage_floats_match_the_reference(surface, fmt, tmp_path):
+    x = GOLDEN[f"narrow_{fmt}_x"]
+    x.astype(np.float64).tofile(tmp_path / "x")
+    assert run(surface, "narrow", fmt, str(tmp_path / "x"), str(tmp_path / "y")).returncode == 0
+    assert np.array_equal(np.fromfile(tmp_path / "y", np.uint32), GOLDEN[f"narrow_{fmt}_bits"])
+
+    q = np.stack([GOLDEN[f"quantize_{fmt}_x"], GOLDEN[f"quantize_{fmt}_scale"]], axis=1).astype(np.float32)
+    q.tofile(tmp_path / "q")
+    assert run(surface, "quantize", fmt, str(tmp_path / "q"), str(tmp_path / "r")).returncode == 0
+    assert np.array_equal(np.fromfile(tmp_path / "r", np.uint32), GOLDEN[f"quantize_{fmt}_bits"])
+
+    GOLDEN[f"decode_{fmt}_bits"].astype(np.uint32).tofile(tmp_path / "p")
+    assert run(surface, "decode", fmt, str(tmp_path / "p"), str(tmp_path / "v")).returncode == 0
+    got, want = np.fromfile(tmp_path / "v", np.float64), GOLDEN[f"decode_{fmt}_value"]
+    assert np.array_equal(got.view(np.uint64), want.view(np.uint64))  # NaN payloads and signed zeros included
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_the_host_multiply_is_the_reference_loop(surface, fmt, tmp_path):
+    keys = sorted({k.rsplit("_", 1)[0] for k in GOLDEN.files if k.startswith((f"mma_{fmt}_", f"tile_{fmt}_"))})
+    if fmt == "f16":
+        keys += ["app_layer", "app_order"]
+    assert len(keys) >= 14
+    for key in keys:
+        m, n, k = (int(v) for v in GOLDEN[key + "_shape"])
+        for part in ("a", "b", "c"):
+            GOLDEN[f"{key}_{part}"].tofile(tmp_path / part)
+        done = run(surface, "mma", fmt, str(m), str(n), str(k), *(str(tmp_path / p) for p in ("a", "b", "c")),
+                   str(tmp_path / "out"))  # fmt: skip
+        assert done.returncode == 0, (key, done.stderr)
+        got = np.fromfile(tmp_path / "out", np.float32)
+        assert np.array_equal(got.view(np.uint32), GOLDEN[key + "_out"].view(np.uint32)), key
