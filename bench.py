@@ -161,6 +161,71 @@ def bench_mlp(stream, steps, warmup) -> dict:
     return out
 
 
+COPY_BYTES = 1 << 30
+
+
+def bench_traffic(stream, launches: int = 3) -> dict:
+    """The program the two counter passes profile (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): `launches` launches
+    of the dominant kernel on the bench's own 4096^3 bf16 problem, then `launches` device-to-device copies of
+    COPY_BYTES, whose counter readings against their known bytes (COPY_BYTES read, COPY_BYTES written) give the
+    scale from the counters' KiB to bytes moved."""
+    rng = np.random.default_rng(20261201)
+    d, bufs = square(L.BF16, L.BF16, 4096, rng)
+    name = L.select(d)["name"]
+    for _ in range(launches):
+        L.run(d, stream.handle)
+    stream.synchronize()
+    src, dst = hip.Buffer(COPY_BYTES), hip.Buffer(COPY_BYTES)
+    src.zero()
+    hip.synchronize()
+    for _ in range(launches):
+        dst.copy_from(src)
+    hip.synchronize()
+    for b in (*bufs, src, dst):
+        b.close()
+    return {"kernel": name, "launches": launches, "copy_bytes": COPY_BYTES}
+
+
+TRAFFIC = ROOT / "profiles" / "traffic_pipe_bf16_4096.md"
+
+
+def measured_traffic(kernel: str) -> dict | None:
+    """HBM bytes per launch of `kernel` on the 4096^3 bf16 problem, as the committed counter passes found them: the
+    summary's `traffic:` line (kernel name, FETCH bytes, WRITE bytes, both already scaled by the copy). None when the
+    summary is absent or measured another kernel."""
+    if not TRAFFIC.exists():
+        return None
+    for line in TRAFFIC.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 4 and parts[0] == "traffic:" and parts[1] == kernel:
+            fetch, write = int(parts[2]), int(parts[3])
+            return {"bytes": fetch + write, "fetch": fetch, "write": write}
+    return None
+
+
+def summarize(directory: Path) -> None:
+    """Tables from rocprofv3's CSV output in `directory` (--output-format csv): per kernel and grid, the launch count
+    and durations from *_kernel_trace.csv; per dispatch, the counter readings from *_counter_collection.csv."""
+    import csv
+
+    for path in sorted(directory.glob("*_kernel_trace.csv")):
+        groups: dict[tuple, list[int]] = {}
+        for r in csv.DictReader(path.open()):
+            key = (r["Kernel_Name"], int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+            groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        print(f"{path.name}: kernel | grid (threads) | launches | average us | median us | min us")
+        for (name, grid), ns in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            ns.sort()
+            print(f"{name} | {grid} | {len(ns)} | {sum(ns) / len(ns) / 1e3:.1f} | {ns[len(ns) // 2] / 1e3:.1f} | "
+                  f"{ns[0] / 1e3:.1f}")  # fmt: skip
+    for path in sorted(directory.glob("*_counter_collection.csv")):
+        print(f"{path.name}: dispatch | kernel | grid (threads) | counter | value (KiB) | duration us")
+        for r in csv.DictReader(path.open()):
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            print(f"{r['Dispatch_Id']} | {r['Kernel_Name']} | {r['Grid_Size']} | {r['Counter_Name']} | "
+                  f"{float(r['Counter_Value']):.1f} | {us:.1f}")  # fmt: skip
+
+
 def cpu_baseline(seconds: float = 12.0) -> dict | None:
     """The reference's host multiply (cr::tensor::multiply<bf16>, single thread, the reference's own header compiled
     into oracle/_ref) on a bounded bf16 sample, repeated in blocks, median of the blocks. Falls back to the oracle's
@@ -206,9 +271,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["square", "skinny", "mlp", "all"], default="all")
+    ap.add_argument("--only", choices=["square", "skinny", "mlp", "all", "traffic"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)  # fmt: skip
@@ -217,6 +286,10 @@ def main() -> int:
     dev = hip.describe(0)
     log("device", dev)
     stream = hip.Stream()
+    if args.only == "traffic":
+        print(json.dumps({"traffic_run": bench_traffic(stream)}), flush=True)
+        stream.close()
+        return 0
     record = {"metric": "bf16 GEMM TFLOP/s at 4096^3 + int8 TOPS, % of MFMA peak, 1 MI355X", "unit": "TFLOP/s",
               "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
               "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded normal)",
@@ -226,9 +299,14 @@ def main() -> int:
         bf, i8 = bench_square(stream, args.steps, args.warmup)
         record["value"] = bf["tflops"]
         record["ms_per_step"] = bf["wall_ms_per_step"]
+        traffic = measured_traffic(bf["kernel"])
         record["roofline"] = {"bound": "mfma", "achieved": bf["kernel_tflops"], "peak": PEAK_BF16, "unit": "TFLOP/s",
-                              "frac": bf["kernel_tflops"] / PEAK_BF16, "traffic": None,
-                              "kernel": bf["kernel"]}  # fmt: skip
+                              "frac": bf["kernel_tflops"] / PEAK_BF16,
+                              "traffic": traffic["bytes"] if traffic else None,
+                              "algorithmic_bytes": 3 * 4096 * 4096 * 2, "kernel": bf["kernel"]}  # fmt: skip
+        if traffic:
+            record["roofline"]["traffic_split"] = {"fetch": traffic["fetch"], "write": traffic["write"],
+                                                   "source": str(TRAFFIC.relative_to(ROOT))}  # fmt: skip
         record["int8"] = {"metric": "int8 W8A8 4096^3 TOPS (dequant to bf16)", **i8}
         log(f"bf16 {bf['tflops']:.0f} TFLOP/s ({bf['kernel_tflops'] / PEAK_BF16:.1%}); int8 {i8['tops']:.0f} TOPS")
     if args.only in ("skinny", "all"):
