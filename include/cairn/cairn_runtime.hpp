@@ -7,6 +7,13 @@
 #include <cstdio>
 #include <cstdlib>
 
+// Host-and-device functions: CR_HD marks what both compile (the spelling of src/cairn/runtime/cairn_runtime.hpp:18-24).
+#if defined(__HIPCC__)
+#define CR_HD __host__ __device__
+#else
+#define CR_HD
+#endif
+
 namespace cr {
 
 [[noreturn]] inline void trap() noexcept { std::abort(); }

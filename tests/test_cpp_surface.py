@@ -74,3 +74,22 @@ def test_the_host_multiply_is_the_reference_loop(surface, fmt, tmp_path):
         assert done.returncode == 0, (key, done.stderr)
         got = np.fromfile(tmp_path / "out", np.float32)
         assert np.array_equal(got.view(np.uint32), GOLDEN[key + "_out"].view(np.uint32)), key
+
+
+def test_emitted_code_builds_against_the_include_set_and_the_library(tmp_path):
+    """An emitted-shaped unit (tests/cpp/emitted.cpp) compiles with g++ on include/cairn alone and links against the
+    library: the spellings emitted code uses (cr::tensor::launch, cr::gpu::here, cr::view, cr::disjoint,
+    cr::gpu::Enqueued, the storage floats) all resolve."""
+    from cairn_amd import lib as L
+
+    L.load()
+    rocm = Path("/opt/rocm")
+    exe = tmp_path / "emitted"
+    subprocess.run(["g++", "-std=c++20", "-O2", "-ffp-contract=off", "-fno-exceptions", "-fno-rtti", "-Wall", "-Wextra",
+                    "-Werror", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include' / 'cairn'}", f"-I{rocm / 'include'}",
+                    str(ROOT / "tests" / "cpp" / "emitted.cpp"), "-o", str(exe), f"-L{L.LIBRARY.parent}",
+                    f"-l:{L.LIBRARY.name}", f"-L{rocm / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{L.LIBRARY.parent}"],
+                   check=True)  # fmt: skip
+    syms = subprocess.run(["nm", str(exe)], capture_output=True, text=True, check=True).stdout
+    assert "cf_emitted_mma" in syms and "cq_emitted_mma" in syms
+    assert "cairn_gemm_mma" in subprocess.run(["nm", "-u", str(exe)], capture_output=True, text=True).stdout
