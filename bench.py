@@ -88,11 +88,14 @@ def square(ab: int, out: int, n: int, rng, **kw) -> tuple[L.Desc, list]:
     return d, bufs
 
 
-def bench_square(stream, steps, warmup) -> tuple[dict, dict]:
+def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict, dict]:
+    """bf16 and int8 4096^3 on the selector's kernels, or on the 256 x 256 NN kernel of `family` when named."""
     rng = np.random.default_rng(20261201)
     n = 4096
     flops = 2.0 * n**3
+    named = (lambda t: L.kernel_named(f"cairn_{family}_{t}_nn_256x256")) if family else (lambda t: 0)
     d, bufs = square(L.BF16, L.BF16, n, rng)
+    d.kernel = named("bf16")
     choice = L.select(d)
     log("bf16 4096^3 on", choice["name"])
     t = timed([d], stream, steps, warmup)
@@ -101,6 +104,7 @@ def bench_square(stream, steps, warmup) -> tuple[dict, dict]:
     for x in bufs:
         x.close()
     d, bufs = square(L.I8, L.BF16, n, rng, row_scale=True)
+    d.kernel = named("i8")
     choice = L.select(d)
     log("int8 4096^3 on", choice["name"])
     t = timed([d], stream, steps, warmup)
@@ -164,13 +168,15 @@ def bench_mlp(stream, steps, warmup) -> dict:
 COPY_BYTES = 1 << 30
 
 
-def bench_traffic(stream, launches: int = 3) -> dict:
+def bench_traffic(stream, launches: int = 3, family: str | None = None) -> dict:
     """The program the two counter passes profile (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): `launches` launches
     of the dominant kernel on the bench's own 4096^3 bf16 problem, then `launches` device-to-device copies of
     COPY_BYTES, whose counter readings against their known bytes (COPY_BYTES read, COPY_BYTES written) give the
     scale from the counters' KiB to bytes moved."""
     rng = np.random.default_rng(20261201)
     d, bufs = square(L.BF16, L.BF16, 4096, rng)
+    if family:
+        d.kernel = L.kernel_named(f"cairn_{family}_bf16_nn_256x256")
     name = L.select(d)["name"]
     for _ in range(launches):
         L.run(d, stream.handle)
@@ -273,6 +279,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", choices=["square", "skinny", "mlp", "all", "traffic"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--family", choices=["pipe", "wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
     args = ap.parse_args()
     if args.summarize:
@@ -287,7 +294,7 @@ def main() -> int:
     log("device", dev)
     stream = hip.Stream()
     if args.only == "traffic":
-        print(json.dumps({"traffic_run": bench_traffic(stream)}), flush=True)
+        print(json.dumps({"traffic_run": bench_traffic(stream, family=args.family)}), flush=True)
         stream.close()
         return 0
     record = {"metric": "bf16 GEMM TFLOP/s at 4096^3 + int8 TOPS, % of MFMA peak, 1 MI355X", "unit": "TFLOP/s",
@@ -296,7 +303,7 @@ def main() -> int:
               "config": {"workload": "bf16 GEMM 4096x4096x4096 NN, fp32 accumulate, bf16 out (BASELINE configs[1])",
                          "m": 4096, "n": 4096, "k": 4096, "layout": "NN", "parallelism": "none (1 GPU)"}}  # fmt: skip
     if args.only in ("square", "all"):
-        bf, i8 = bench_square(stream, args.steps, args.warmup)
+        bf, i8 = bench_square(stream, args.steps, args.warmup, args.family)
         record["value"] = bf["tflops"]
         record["ms_per_step"] = bf["wall_ms_per_step"]
         traffic = measured_traffic(bf["kernel"])

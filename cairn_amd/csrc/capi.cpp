@@ -17,6 +17,9 @@ using Launcher = hipError_t (*)(const Params&, hipStream_t);
 #define CAIRN_PIPE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
 #include "pipe_instances.inc"
 #undef CAIRN_PIPE_INSTANCE
+#define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
+#include "wave_instances.inc"
+#undef CAIRN_WAVE_INSTANCE
 hipError_t cairn_generic(const Params&, hipStream_t);
 hipError_t cairn_skinny(const Params&, hipStream_t, int split);
 
@@ -25,7 +28,7 @@ namespace {
 constexpr int CUS = 256;              // gfx950: 8 XCDs of 32 CUs (MI350X, MI355X)
 constexpr int LDS_PER_CU = 160 * 1024;
 
-enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2, PIPE = 3 };
+enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2, PIPE = 3, WAVE = 4 };
 
 struct Kernel {
   Launcher run;
@@ -39,14 +42,17 @@ struct Kernel {
 
 #define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) {NAME, MFMA, OP, TA, TB, BM, BN, #NAME, 2},
 #define CAIRN_PIPE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, PIPE, OP, TA, TB, BM, BN, #NAME, STAGES},
+#define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, WAVE, OP, TA, TB, BM, BN, #NAME, STAGES},
 const Kernel TABLE[] = {
     {nullptr, GENERIC, -1, false, false, 64, 64, "cairn_generic_64x64", 1},
     {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 32, "cairn_skinny_bf16_nt", 0},
 #include "instances.inc"
 #include "pipe_instances.inc"
+#include "wave_instances.inc"
 };
 #undef CAIRN_MFMA_INSTANCE
 #undef CAIRN_PIPE_INSTANCE
+#undef CAIRN_WAVE_INSTANCE
 constexpr int COUNT = int(sizeof(TABLE) / sizeof(TABLE[0]));
 
 int op_of(int type) {
@@ -120,10 +126,11 @@ bool mfma_fits(const cairn_gemm_desc& d, const Kernel& k) {
   return a_ok && b_ok && c_ok;
 }
 
-// Can the pipelined kernel take it: 16-byte loads whole and aligned (K-major rows in chunks of 16 bytes of k; M/N-major
-// rows in chunks of 16 bytes of columns), offsets inside int32.
+// Can a kernel of the LDS ring (pipelined, or one wave a SIMD) take it: 16-byte loads whole and aligned (K-major rows
+// in chunks of 16 bytes of k; M/N-major rows in chunks of 16 bytes of columns), offsets inside int32.
+bool ring(const Kernel& k) { return k.family == PIPE || k.family == WAVE; }
 bool pipe_fits(const cairn_gemm_desc& d, const Kernel& k) {
-  if(k.family != PIPE || k.op != op_of(d.ab_type) || k.ta != bool(d.trans_a) || k.tb != bool(d.trans_b)) return false;
+  if(!ring(k) || k.op != op_of(d.ab_type) || k.ta != bool(d.trans_a) || k.tb != bool(d.trans_b)) return false;
   const int es = element_size(d.ab_type), ce = 16 / es;
   const std::uint64_t bk = 64 / es;
   auto kmajor = [&](const void* p, std::uint64_t ld, int rows) {
@@ -136,10 +143,14 @@ bool pipe_fits(const cairn_gemm_desc& d, const Kernel& k) {
   const bool b_ok = d.trans_b ? kmajor(d.b, d.ldb, k.bn) : mnmajor(d.b, d.ldb, d.n);
   const int os = output_size(d.c_type);
   const bool c_ok = d.n % 4 == 0 && d.ldc % 4 == 0 && aligned(d.c, 4 * os);
-  return a_ok && b_ok && c_ok;
+  // The one-wave-a-SIMD kernel loads by immediate offsets (pipe.hpp, Loader::imm_fits): a K-major operand's rows at
+  // least a stage's 64 bytes apart, an M/N-major operand's k rows at least a tile's width of elements apart.
+  auto imm = [&](bool kmaj, std::uint64_t ld, int width) { return kmaj ? ld * es >= 64 : ld >= std::uint64_t(width); };
+  const bool imm_ok = k.family != WAVE || (imm(!d.trans_a, d.lda, k.bm) && imm(bool(d.trans_b), d.ldb, k.bn));
+  return a_ok && b_ok && c_ok && imm_ok;
 }
 
-bool tiled_fits(const cairn_gemm_desc& d, const Kernel& k) { return k.family == PIPE ? pipe_fits(d, k) : mfma_fits(d, k); }
+bool tiled_fits(const cairn_gemm_desc& d, const Kernel& k) { return ring(k) ? pipe_fits(d, k) : mfma_fits(d, k); }
 
 // The skinny kernel: bf16, b stored n x k (the decode layout), m <= 16, every row 16-byte whole.
 bool skinny_fits(const cairn_gemm_desc& d) {
@@ -150,12 +161,12 @@ bool skinny_fits(const cairn_gemm_desc& d) {
 
 // Workgroups of a tile shape one CU holds at once: LDS is the limit (two stages of both operands).
 int lds_bytes(const Kernel& k) {
-  if(k.family == PIPE) return k.stages * (k.bm + k.bn) * 64;
+  if(ring(k)) return k.stages * (k.bm + k.bn) * 64;
   if(k.family == MFMA) return 2 * (k.bm + k.bn) * 128;
   return k.family == GENERIC ? 4096 : 8192;
 }
 int resident(const Kernel& k) {
-  if(k.family != MFMA && k.family != PIPE) return 8;
+  if(k.family != MFMA && !ring(k)) return 8;
   const int lds = lds_bytes(k);
   return std::max(1, std::min(2, LDS_PER_CU / lds));
 }
@@ -165,6 +176,7 @@ int resident(const Kernel& k) {
 double shape_rate(const Kernel& k) {
   const int area = k.bm * k.bn;
   if(k.family == PIPE) return area >= 256 * 256 ? 2.0 : (area >= 256 * 128 ? 1.8 : 1.5);
+  if(k.family == WAVE) return area >= 256 * 256 ? 1.9 : (area >= 256 * 128 ? 1.7 : 1.4);
   if(area >= 256 * 256) return 1.0;
   if(area >= 256 * 128) return 0.92;
   return 0.78;
@@ -172,7 +184,7 @@ double shape_rate(const Kernel& k) {
 
 // k elements a k-step of the kernel covers.
 int tile_k(const Kernel& k) {
-  const int bytes = k.family == MFMA ? 128 : (k.family == PIPE ? 64 : 32);
+  const int bytes = k.family == MFMA ? 128 : (ring(k) ? 64 : 32);
   if(k.family == SKINNY) return 32;
   return k.op == cairn::gemm::OP_I8 ? bytes : bytes / 2;
 }

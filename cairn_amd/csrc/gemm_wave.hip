@@ -1,0 +1,247 @@
+// The one-wave-a-SIMD MFMA GEMM for gfx950: four waves per workgroup, each feeding its SIMD's matrix core without a
+// partner wave, with the LDS reads of its next MFMA k-step and the loads of a later stage issued between its MFMAs.
+//
+// A workgroup of 256 threads computes one BM x BN output tile (256 x 256 by default); wave w holds the (BM/2) x
+// (BN/2) block at wave_origin (pipe.hpp), 4 x 4 blocks of 32 x 32 accumulators at 256 x 256, which live in the
+// accumulation registers. The operand stages are the ones the eight-wave kernel (gemm_pipe.hip) uses: 64 bytes of k of
+// every operand row a stage, STAGES deep, filled by buffer_load ... lds, with the same swizzles and fragment reads;
+// here all four waves load both operands, a quarter each.
+//
+// Compared with eight waves of (BM/2) x (BN/4), a wave's larger block reads a third less from LDS for the same MFMA
+// work (a stage is read 2 + 2 times, not 4 + 2), and the workgroup meets at one barrier a stage instead of two.
+//
+// Iteration `it` works on stage it in two MFMA k-steps, the operands double-buffered in registers:
+//   k-step 0: the 16 MFMAs of (it, 0), between them the fragment reads of (it, 1) and b's loads of stage
+//             it + STAGES - 1;
+//             wait for this wave's LDS reads and for its loads of stage it + 1; barrier;
+//   k-step 1: the 16 MFMAs of (it, 1), between them the fragment reads of (it + 1, 0) and a's loads of stage
+//             it + STAGES, into the buffer stage it used.
+// The barrier orders both hazards of the ring. Past it every wave's loads of stage it + 1 have landed (each waited
+// for its own), and every wave's reads of stage it are complete (each waited for its own LDS reads, and its last reads
+// of stage it were those of (it, 1)): so stage it's buffer is free from then on, and its refill is spread over the
+// next 32 MFMAs, one 16-byte load a lane every fourth MFMA. A wave's loads of one operand's stage fill consecutive
+// KiB of LDS (pipe.hpp, slot), so M0 is written once per operand and stage and each load picks its KiB with its
+// immediate offset: a write of M0 waits for the wave's previous LDS load to leave the queue, and one per load cost a
+// quarter of the loop (measured). The host runs this kernel only where no lane's offset register would go below zero
+// (Loader::imm_fits).
+// Every iteration issues its loads: past the last stage they read nothing (the buffer resource's range is empty)
+// and land in a buffer no later stage uses, so the loop has no branches and the wait for stage it + 1 is the same
+// count every time. Scheduling fences keep the interleave as written and keep everything on its side of the barrier.
+// No atomics: the result's bits do not depend on timing.
+#include <hip/hip_runtime.h>
+#include <utility>
+#include "kernels.hpp"
+#include "mfma.hpp"
+#include "pipe.hpp"
+#include "ring.hpp"
+#include "tile.hpp"
+
+namespace cairn::gemm {
+using namespace cairn::pipe;
+
+// f(integral_constant<I>) for I = 0 .. N-1, in order.
+template<int N, class F> __device__ __forceinline__ void unrolled(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
+}
+
+// No instruction is scheduled across this point.
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+
+__device__ __forceinline__ void fenced_barrier() {
+  fence();
+  asm volatile("s_barrier" ::: "memory");
+  fence();
+}
+
+template<class Sh, int OP, bool TA, bool TB>
+__global__ void __launch_bounds__(256) wave_gemm(Params p) {
+  static_assert(Sh::WAVES == 4, "one wave a SIMD");
+  using M = Mfma<OP>;
+  using Acc = typename M::Acc;
+  constexpr bool AK = !TA, BKM = TB;
+  constexpr int S = Sh::STAGES, FM = Sh::FM, FN = Sh::FN, ES = Sh::ES;
+  constexpr int LOADS = Sh::LOADS_A + Sh::LOADS_B;  // this thread's 16-byte loads a stage
+  constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, READS = RA + RB;  // LDS reads a k-step
+  static_assert(READS <= 32 && LOADS <= 8, "the interleave below places these between 16 MFMAs");
+  __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  int wr, wc;
+  wave_origin<Sh>(wave, wr, wc);
+  int tm, tn;
+  cairn::tile::tile_of(int(blockIdx.x), p.tiles_m, p.tiles_n, p.group, tm, tn);
+  const int row0 = tm * Sh::BM, col0 = tn * Sh::BN;
+  const cairn::tile::Panel pa = cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES);
+  const cairn::tile::Panel pb = cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES);
+  const char* a = static_cast<const char*>(p.a) + pa.start;
+  const char* b = static_cast<const char*>(p.b) + pb.start;
+  const unsigned ring = lds_address(lds);
+
+  Dma dma;
+  Loader<Sh, Sh::BM, AK, Dma> la;
+  Loader<Sh, Sh::BN, BKM, Dma> lb;  // the host runs this kernel only where both loaders' imm_fits holds
+  la.setup(t, row0, p.m, p.lda);
+  lb.setup(t, col0, p.n, p.ldb);
+  const int T = (p.k + Sh::BK - 1) / Sh::BK;
+
+  Acc acc[FM][FN];
+#pragma unroll
+  for(int i = 0; i < FM; ++i)
+#pragma unroll
+    for(int j = 0; j < FN; ++j) acc[i][j] = Acc{};
+  u32x4 xa[2][FM], xb[2][FN];
+
+  // Read X of a k-step's READS: a's fragments first (one b128 each, or two transpose halves), then b's.
+  auto read = [&](auto buf, const char* stage, int s, auto x) {
+    constexpr int X = decltype(x)::value, BUF = decltype(buf)::value;
+    if constexpr(X < RA) {
+      if constexpr(AK) xa[BUF][X] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(wr + 32 * X, s, lane));
+      else {
+        const u32x2 h = transpose_half<ES>(stage + mnmajor_fragment<ES, Sh::BM>(wr + 32 * (X / 2), s, X % 2, lane));
+        xa[BUF][X / 2][2 * (X % 2)] = h[0];
+        xa[BUF][X / 2][2 * (X % 2) + 1] = h[1];
+      }
+    } else {
+      constexpr int Y = X - RA;
+      const char* bs = stage + Sh::A_BYTES;
+      if constexpr(BKM) xb[BUF][Y] = *reinterpret_cast<const u32x4*>(bs + kmajor_fragment(wc + 32 * Y, s, lane));
+      else {
+        const u32x2 h = transpose_half<ES>(bs + mnmajor_fragment<ES, Sh::BN>(wc + 32 * (Y / 2), s, Y % 2, lane));
+        xb[BUF][Y / 2][2 * (Y % 2)] = h[0];
+        xb[BUF][Y / 2][2 * (Y % 2) + 1] = h[1];
+      }
+    }
+  };
+  auto mfma = [&](auto buf, auto x) {
+    constexpr int X = decltype(x)::value, BUF = decltype(buf)::value, I = X / FN, J = X % FN;
+    acc[I][J] = M::step(xb[BUF][J], xa[BUF][I], acc[I][J]);
+  };
+  auto stage_of = [&](int st) { return lds + (st % S) * Sh::STAGE; };
+  using LA = Loader<Sh, Sh::BM, AK, Dma>;
+  using LB = Loader<Sh, Sh::BN, BKM, Dma>;
+  auto at_of = [&](int st) { return ring + unsigned((st % S) * Sh::STAGE); };
+  // One operand's part of a stage: M0 once, then its loads by immediate offset.
+  auto load_a = [&](const auto& r, int st, auto u) {
+    if constexpr(decltype(u)::value == 0) dma.set_base(LA::base(at_of(st), wave));
+    la.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  };
+  auto load_b = [&](const auto& r, int st, auto u) {
+    if constexpr(decltype(u)::value == 0) dma.set_base(LB::base(at_of(st) + Sh::A_BYTES, wave));
+    lb.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  };
+  auto stage_a = [&](int st) {
+    const auto r = la.resource(dma, a, pa.bytes, p.lda, st);
+    unrolled<Sh::LOADS_A>([&](auto u) { load_a(r, st, u); });
+  };
+  auto stage_b = [&](int st) {
+    const auto r = lb.resource(dma, b, pb.bytes, p.ldb, st);
+    unrolled<Sh::LOADS_B>([&](auto u) { load_b(r, st, u); });
+  };
+
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  // Stages 0 .. S - 2 whole and a's part of stage S - 1; iteration 0 brings b's part of stage S - 1.
+  for(int st = 0; st < S - 1; ++st) {
+    stage_a(st);
+    stage_b(st);
+  }
+  stage_a(S - 1);
+  wait_loads<(S - 2) * LOADS + Sh::LOADS_A>();
+  fenced_barrier();
+  unrolled<READS>([&](auto x) { read(B0{}, stage_of(0), 0, x); });
+
+  // Placing: reads 2 X and 2 X + 1 of a k-step after MFMA X, so that they complete well before their MFMAs; load u of
+  // a half stage after MFMA 4 u + 2.
+  static_assert(Sh::LOADS_A <= 4 && Sh::LOADS_B <= 4, "a half stage's loads take every fourth MFMA");
+  for(int it = 0; it < T; ++it) {
+    const char* cur = stage_of(it);
+    const char* nxt = stage_of(it + 1);
+    const int sb = it + S - 1, sa = it + S;  // the stages whose b's, then a's, loads this iteration issues
+    const auto rb = lb.resource(dma, b, pb.bytes, p.ldb, sb);
+    unrolled<16>([&](auto x) {
+      constexpr int X = decltype(x)::value;
+      mfma(B0{}, x);
+      fence();
+      if constexpr(2 * X < READS) read(B1{}, cur, 1, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(B1{}, cur, 1, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_B) load_b(rb, sb, std::integral_constant<int, X / 4>{});
+      fence();
+    });
+    const auto ra = la.resource(dma, a, pa.bytes, p.lda, sa);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    wait_loads<(S - 2) * LOADS>();
+    fenced_barrier();
+    unrolled<16>([&](auto x) {
+      constexpr int X = decltype(x)::value;
+      mfma(B1{}, x);
+      fence();
+      if constexpr(2 * X < READS) read(B0{}, nxt, 0, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(B0{}, nxt, 0, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_A) load_a(ra, sa, std::integral_constant<int, X / 4>{});
+      fence();
+    });
+  }
+  wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
+
+  // Epilogue: block (i, j) of this wave, quad q of lane l: row m, columns n .. n+3. A plain bf16 output (no scales,
+  // bias or activation) takes the packed conversion, and a tile wholly inside c skips the bounds checks.
+  const bool plain = !p.row_scale && !p.col_scale && !p.bias && p.act == CAIRN_ACT_NONE;
+  if(OP != OP_I8 && plain && p.c_type == CAIRN_TYPE_BF16) {
+    char* c = static_cast<char*>(p.c);
+    const bool whole = row0 + Sh::BM <= p.m && col0 + Sh::BN <= p.n;
+    auto quad = [&](int i, int j, int q, bool check) {
+      const int m = row0 + wr + 32 * i + cairn::tile::acc_m(lane);
+      const int n = col0 + wc + 32 * j + cairn::tile::acc_n(lane, q);
+      if(check && !(m < p.m && n < p.n)) return;
+      u32x2 w;
+      w[0] = narrow2_bf16(float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]));
+      w[1] = narrow2_bf16(float(acc[i][j][4 * q + 2]), float(acc[i][j][4 * q + 3]));
+      *reinterpret_cast<u32x2*>(c + (std::int64_t(m) * p.ldc + n) * 2) = w;
+    };
+    if(whole) {
+#pragma unroll
+      for(int i = 0; i < FM; ++i)
+#pragma unroll
+        for(int j = 0; j < FN; ++j)
+#pragma unroll
+          for(int q = 0; q < 4; ++q) quad(i, j, q, false);
+    } else {
+#pragma unroll
+      for(int i = 0; i < FM; ++i)
+#pragma unroll
+        for(int j = 0; j < FN; ++j)
+#pragma unroll
+          for(int q = 0; q < 4; ++q) quad(i, j, q, true);
+    }
+    return;
+  }
+#pragma unroll
+  for(int i = 0; i < FM; ++i) {
+    const int m = row0 + wr + 32 * i + cairn::tile::acc_m(lane);
+#pragma unroll
+    for(int j = 0; j < FN; ++j)
+#pragma unroll
+      for(int q = 0; q < 4; ++q) {
+        const int n = col0 + wc + 32 * j + cairn::tile::acc_n(lane, q);
+        if(m < p.m && n < p.n) store_quad(p, m, n, acc[i][j], q);
+      }
+  }
+}
+
+template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave(const Params& p, hipStream_t s) {
+  const unsigned grid = unsigned(p.tiles_m) * unsigned(p.tiles_n);
+  hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace cairn::gemm
+
+#define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB)                                                      \
+  hipError_t NAME(const cairn::gemm::Params& p, hipStream_t s) {                                                 \
+    return cairn::gemm::launch_wave<                                                                              \
+        cairn::pipe::Shape<BM, BN, (OP == cairn::gemm::OP_I8 ? 1 : 2), STAGES, 4>, OP, TA, TB>(p, s);           \
+  }
+#include "wave_instances.inc"

@@ -43,6 +43,14 @@ __device__ inline std::uint16_t narrow_bf16(float x) {
   if((u & 0x7fffffffu) > 0x7f800000u) return std::uint16_t(((u >> 16) & 0x8000u) | 0x7fc0u);
   return std::uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
+// Two f32 -> bf16 in one instruction (v_cvt_pk_bf16_f32: nearest even, subnormals kept as the kernels' f32 mode
+// keeps them, overflow to infinity), x in the low half. Equal to narrow_bf16 on every finite value and every infinity;
+// a NaN stays a NaN, its payload the instruction's (the multiply's contract promises no particular NaN).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ inline std::uint32_t narrow2_bf16(float x, float y) {
+  const bf16x2_t v = {static_cast<__bf16>(x), static_cast<__bf16>(y)};
+  return __builtin_bit_cast(std::uint32_t, v);
+}
 // f32 -> f16, round to nearest even (the conversion's mode), overflow to infinity.
 __device__ inline std::uint16_t narrow_f16(float x) {
   const _Float16 h = static_cast<_Float16>(x);

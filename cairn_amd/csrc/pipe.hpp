@@ -28,24 +28,41 @@
 namespace cairn::pipe {
 using cairn::tile::u32x4;
 
-template<int BM_, int BN_, int ES_, int STAGES_> struct Shape {
-  static constexpr int BM = BM_, BN = BN_, ES = ES_, STAGES = STAGES_;
+// WAVES 8: two groups of four waves (gemm_pipe.hip), a wave holding (BM/2) x (BN/4) outputs; WAVES 4: one wave a
+// SIMD (gemm_wave.hip), a wave holding (BM/2) x (BN/2). Either way a stage's loads are spread over 256 threads: one
+// group's for one operand (8 waves), or all four waves' for both (4 waves).
+template<int BM_, int BN_, int ES_, int STAGES_, int WAVES_ = 8> struct Shape {
+  static constexpr int BM = BM_, BN = BN_, ES = ES_, STAGES = STAGES_, WAVES = WAVES_;
   static constexpr int ROW = 64;             // bytes of k per operand row per stage
   static constexpr int BK = ROW / ES;        // k elements per stage: 32 or 64
   static constexpr int CE = 16 / ES;         // k elements per 16-byte chunk of a K-major row
-  static constexpr int THREADS = 512, GROUP = 256;
-  static constexpr int WTM = BM / 2, WTN = BN / 4;  // a wave's outputs: group g holds rows g * BM/2 ..
+  static constexpr int THREADS = 64 * WAVES, GROUP = 256;
+  static constexpr int WTM = BM / 2, WTN = WAVES == 8 ? BN / 4 : BN / 2;  // a wave's outputs
   static constexpr int FM = WTM / 32, FN = WTN / 32;
   static constexpr int STEPS = 2;            // MFMA k-steps per stage
   static constexpr int A_BYTES = BM * ROW, B_BYTES = BN * ROW, STAGE = A_BYTES + B_BYTES;
   static constexpr int LOADS_A = BM * 4 / GROUP, LOADS_B = BN * 4 / GROUP;  // 16-byte loads per thread per stage
-  static_assert(BM % 64 == 0 && BN % 128 == 0, "whole 32 x 32 blocks for every wave");
+  static_assert(WAVES == 8 || WAVES == 4, "two groups of four waves, or one wave a SIMD");
+  static_assert(BM % 64 == 0 && BN % (WAVES == 8 ? 128 : 64) == 0, "whole 32 x 32 blocks for every wave");
   static_assert(STAGES >= 3 && STAGES * STAGE <= 160 * 1024, "the ring fits the CU's LDS");
 };
 
-// The 16-byte LDS slot load u of thread t (0..255 within its loading group) writes: 16 q bytes into the operand's
-// stage, q = (4 u + wave) * 64 + lane.
-CAIRN_HD int slot(int t, int u) { return (u * 4 + (t >> 6)) * 64 + (t & 63); }
+// The tile row and column where wave `wave`'s (WTM x WTN) block of accumulators starts: eight waves, group wave / 4
+// over rows and wave % 4 over columns; four waves, a 2 x 2 grid.
+template<class Sh> CAIRN_HD void wave_origin(int wave, int& r, int& c) {
+  if constexpr(Sh::WAVES == 8) {
+    r = (wave >> 2) * Sh::WTM;
+    c = (wave & 3) * Sh::WTN;
+  } else {
+    r = (wave >> 1) * Sh::WTM;
+    c = (wave & 1) * Sh::WTN;
+  }
+}
+
+// The 16-byte LDS slot load u (of LOADS) of thread t (0..255 within its loading group) writes: 16 q bytes into the
+// operand's stage, q = (LOADS wave + u) * 64 + lane. A wave's loads of one operand's stage fill LOADS consecutive KiB,
+// so that one LDS base (M0) serves them all, the load's immediate offset choosing its KiB.
+template<int LOADS> CAIRN_HD int slot(int t, int u) { return ((t >> 6) * LOADS + u) * 64 + (t & 63); }
 
 // K-major: byte of (row r, chunk c), and the (row, chunk) slot q holds.
 CAIRN_HD int kmajor_at(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
@@ -97,7 +114,7 @@ template<class Sh, int R, bool KMAJOR, class Mem> struct Loader {
   CAIRN_HD void setup(int gt, int first, int total, std::int64_t ld) {
 #pragma unroll
     for(int u = 0; u < LOADS; ++u) {
-      const int q = slot(gt, u);
+      const int q = slot<LOADS>(gt, u);
       int r, c;
       if constexpr(KMAJOR) {
         kmajor_slot(q, r, c);
@@ -110,17 +127,40 @@ template<class Sh, int R, bool KMAJOR, class Mem> struct Loader {
       }
     }
   }
-  // Stage `st` of k into LDS at `dst` (this operand's part of the ring buffer).
-  CAIRN_HD void issue(Mem& mem, const char* panel, std::int64_t bytes, std::int64_t ld, int st, int k, char* dst, int w) {
+  // The buffer resource of stage `st`: the panel from the stage's first k on.
+  CAIRN_HD auto resource(Mem& mem, const char* panel, std::int64_t bytes, std::int64_t ld, int st) const {
     const std::int64_t step = KMAJOR ? std::int64_t(st) * Sh::ROW : std::int64_t(st) * Sh::BK * ld * Sh::ES;
-    const auto r = mem.resource(panel + step, bytes - step);
+    return mem.resource(panel + step, bytes - step);
+  }
+  // Load u of stage `st` (resource r) into LDS at `dst` (this operand's part of the stage: a char* or an LDS
+  // address), wave w's share; past k it reads zeros.
+  template<class Rsrc, class Dst>
+  CAIRN_HD void load_one(Mem& mem, const Rsrc& r, Dst dst, int st, int k, int u, int w) const {
     const int k0 = st * Sh::BK;
     const bool tail = k0 + Sh::BK > k;
+    const int o = tail && k0 + kidx[u] >= k ? cairn::tile::OUTSIDE : offset[u];
+    mem.load_lds(r, dst + (LOADS * w + u) * 1024, o);
+  }
+  // The same load with the wave's LDS base for this operand's stage (its first KiB, base()) already set: the load's
+  // immediate offset 1024 U picks its KiB, and the lane's global offset is lowered by as much, which stays at or above
+  // zero where imm_fits holds.
+  template<int U, class Rsrc> CAIRN_HD void load_imm(Mem& mem, const Rsrc& r, int st, int k) const {
+    const int k0 = st * Sh::BK;
+    const bool tail = k0 + Sh::BK > k;
+    const int o = tail && k0 + kidx[U] >= k ? cairn::tile::OUTSIDE : offset[U];
+    mem.template load_lds_imm<U>(r, o);
+  }
+  template<class Dst> CAIRN_HD static Dst base(Dst dst, int w) { return dst + LOADS * w * 1024; }
+  // Whether every lane's offset of load u stays at or above 1024 u for leading dimension ld: the smallest offset of
+  // load u is (wave 0, lane 0) slot 64 u, row 16 u of a K-major operand (64-byte rows a stage), k row
+  // 1024 u / (R ES) of an M/N-major one.
+  CAIRN_HD static bool imm_fits(std::int64_t ld) { return KMAJOR ? ld * Sh::ES >= Sh::ROW : ld >= R; }
+  // Stage `st` of k into LDS at `dst` (this operand's part of the ring buffer).
+  template<class Dst>
+  CAIRN_HD void issue(Mem& mem, const char* panel, std::int64_t bytes, std::int64_t ld, int st, int k, Dst dst, int w) {
+    const auto r = resource(mem, panel, bytes, ld, st);
 #pragma unroll
-    for(int u = 0; u < LOADS; ++u) {
-      const int o = tail && k0 + kidx[u] >= k ? cairn::tile::OUTSIDE : offset[u];
-      mem.load_lds(r, dst + (4 * u + w) * 1024, o);
-    }
+    for(int u = 0; u < LOADS; ++u) load_one(mem, r, dst, st, k, u, w);
   }
 };
 

@@ -17,7 +17,7 @@ F32, F16, BF16, F8E4M3, F8E5M2, I8, I32 = range(7)
 ACT_NONE, ACT_RELU, ACT_GELU = range(3)
 OK, E_SHAPE, E_TYPE, E_KERNEL, E_ARG, E_HIP = range(6)
 DESC_VERSION = 1
-FAMILY = {0: "mfma", 1: "generic", 2: "skinny", 3: "pipe"}
+FAMILY = {0: "mfma", 1: "generic", 2: "skinny", 3: "pipe", 4: "wave"}
 TYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", F8E4M3: "f8e4m3", F8E5M2: "f8e5m2", I8: "i8", I32: "i32"}
 
 

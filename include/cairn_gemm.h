@@ -102,7 +102,8 @@ typedef struct cairn_gemm_kernel {
   int32_t tile_m, tile_n, tile_k; /* output tile and k-step, in elements */
   int32_t threads;       /* per workgroup */
   int32_t lds_bytes;     /* per workgroup */
-  int32_t family;        /* 0: MFMA tiled, 1: generic (any shape), 2: skinny (m <= 16, bandwidth), 3: pipelined */
+  int32_t family;        /* 0: MFMA tiled, 1: generic (any shape), 2: skinny (m <= 16, bandwidth), 3: pipelined,
+                            4: pipelined, one wave a SIMD */
   char name[48];
 } cairn_gemm_kernel;
 

@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <vector>
+#include <utility>
 #include "pipe.hpp"
 #include "tile.hpp"
 
@@ -285,7 +286,20 @@ struct HostDma {
     const u32x4 v = mem->load16(r, offset);
     lds->write16(int(reinterpret_cast<std::uint8_t*>(wave_base) - ring) + 16 * lane, v);
   }
+  // M0 and the immediate offset: the lane's offset register holds offset - 1024 U, which must not go below zero.
+  char* m0 = nullptr;
+  bool negative = false;
+  void set_base(char* base) { m0 = base; }
+  template<int U> void load_lds_imm(Rsrc r, int offset) {
+    if(offset != OUTSIDE && offset - 1024 * U < 0) negative = true;
+    load_lds(r, m0 + 1024 * U, offset);
+  }
 };
+
+template<class L, class D, class R, std::size_t... U>
+void imm_loads(const L& l, D& d, const R& r, int st, int k, std::index_sequence<U...>) {
+  (l.template load_imm<int(U)>(d, r, st, k), ...);
+}
 
 template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad, int group) {
   constexpr int BM = Sh::BM, BN = Sh::BN, ES = Sh::ES;
@@ -327,17 +341,32 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
     for(int st = 0; st < T; ++st) {
       HostLds lds(Sh::STAGE);  // one stage of the ring (the ring's other stages are the same code at other bases)
       HostDma da{&mem_a, &lds, lds.bytes.data()}, db{&mem_b, &lds, lds.bytes.data()};
+      using LA = cairn::pipe::Loader<Sh, BM, AK, HostDma>;
+      using LB = cairn::pipe::Loader<Sh, BN, BKM, HostDma>;
+      // The one-wave-a-SIMD kernel loads through M0 and immediate offsets where the leading dimensions allow it.
+      const bool imm = Sh::WAVES == 4 && LA::imm_fits(lda) && LB::imm_fits(ldb);
+      char* stage_a = reinterpret_cast<char*>(lds.bytes.data());
+      char* stage_b = stage_a + Sh::A_BYTES;
       for(int gt = 0; gt < 256; ++gt) {
         da.lane = db.lane = gt & 63;
-        la[gt].issue(da, a, pa.bytes, lda, st, k, reinterpret_cast<char*>(lds.bytes.data()), gt >> 6);
-        lb[gt].issue(db, b, pb.bytes, ldb, st, k, reinterpret_cast<char*>(lds.bytes.data()) + Sh::A_BYTES, gt >> 6);
+        if(imm) {
+          da.set_base(LA::base(stage_a, gt >> 6));
+          imm_loads(la[gt], da, la[gt].resource(da, a, pa.bytes, lda, st), st, k, std::make_index_sequence<LA::LOADS>{});
+          db.set_base(LB::base(stage_b, gt >> 6));
+          imm_loads(lb[gt], db, lb[gt].resource(db, b, pb.bytes, ldb, st), st, k, std::make_index_sequence<LB::LOADS>{});
+        } else {
+          la[gt].issue(da, a, pa.bytes, lda, st, k, stage_a, gt >> 6);
+          lb[gt].issue(db, b, pb.bytes, ldb, st, k, stage_b, gt >> 6);
+        }
       }
+      if(da.negative || db.negative) FAIL("pipe %s %dx%d es=%d %dx%dx%d: an offset register below zero", lay, BM, BN, ES, m, n, k);
       if(mem_a.bad || mem_b.bad) FAIL("pipe %s %dx%d es=%d %dx%dx%d: a global load outside its matrix", lay, BM, BN, ES, m, n, k);
       if(lds.bad) FAIL("pipe %s: an LDS write off the stage", lay);
       for(int c = 0; c < Sh::STAGE / 16; ++c)
         if(lds.writes[c] != 1) FAIL("pipe %s %dx%d es=%d: LDS chunk %d written %d times", lay, BM, BN, ES, c, lds.writes[c]);
-      for(int wave = 0; wave < 8; ++wave) {
-        const int grp = wave >> 2, w4 = wave & 3;
+      for(int wave = 0; wave < Sh::WAVES; ++wave) {
+        int wr, wc;
+        cairn::pipe::wave_origin<Sh>(wave, wr, wc);
         for(int s = 0; s < 2; ++s)
           for(int i = 0; i < Sh::FM; ++i)
             for(int j = 0; j < Sh::FN; ++j) {
@@ -366,8 +395,8 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
                   }
                 }
               };
-              gather(AK, 0, BM, grp * Sh::WTM + 32 * i, fa);
-              gather(BKM, Sh::A_BYTES, BN, w4 * Sh::WTN + 32 * j, fb);
+              gather(AK, 0, BM, wr + 32 * i, fa);
+              gather(BKM, Sh::A_BYTES, BN, wc + 32 * j, fb);
               if(bad_read) FAIL("pipe %s: a fragment read off its operand's stage", lay);
               if(conflict) FAIL("pipe %s %dx%d es=%d: a fragment read phase has an LDS bank conflict", lay, BM, BN, ES);
               double P[32][32], Q[32][32];
@@ -386,20 +415,21 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
                   const int prow = 8 * (r / 4) + 4 * (l / 32) + r % 4, qcol = l % 32;
                   double sum = 0;
                   for(int kk = 0; kk < 2 * CE; ++kk) sum += P[prow][kk] * Q[kk][qcol];
-                  const int mm = grp * Sh::WTM + 32 * i + acc_m(l);
-                  const int nn = w4 * Sh::WTN + 32 * j + acc_n(l, r / 4) + r % 4;
+                  const int mm = wr + 32 * i + acc_m(l);
+                  const int nn = wc + 32 * j + acc_n(l, r / 4) + r % 4;
                   acc[std::size_t(mm) * BN + nn] += sum;
                 }
             }
       }
     }
-    for(int wave = 0; wave < 8; ++wave) {
-      const int grp = wave >> 2, w4 = wave & 3;
+    for(int wave = 0; wave < Sh::WAVES; ++wave) {
+      int wr, wc;
+      cairn::pipe::wave_origin<Sh>(wave, wr, wc);
       for(int i = 0; i < Sh::FM; ++i)
         for(int j = 0; j < Sh::FN; ++j)
           for(int l = 0; l < 64; ++l)
             for(int q = 0; q < 4; ++q) {
-              const int mm = grp * Sh::WTM + 32 * i + acc_m(l), nn0 = w4 * Sh::WTN + 32 * j + acc_n(l, q);
+              const int mm = wr + 32 * i + acc_m(l), nn0 = wc + 32 * j + acc_n(l, q);
               const int gm = row0 + mm, gn = col0 + nn0;
               if(gm >= m || gn >= n) continue;
               for(int e = 0; e < 4; ++e) {
@@ -463,6 +493,11 @@ int main() {
   pipe_shapes<cairn::pipe::Shape<128, 256, 2, 4>>();
   pipe_shapes<cairn::pipe::Shape<128, 128, 2, 4>>();
   pipe_shapes<cairn::pipe::Shape<128, 128, 1, 4>>();
+  pipe_shapes<cairn::pipe::Shape<256, 256, 2, 4, 4>>();
+  pipe_shapes<cairn::pipe::Shape<256, 256, 1, 4, 4>>();
+  pipe_shapes<cairn::pipe::Shape<256, 128, 2, 4, 4>>();
+  pipe_shapes<cairn::pipe::Shape<128, 128, 2, 4, 4>>();
+  pipe_shapes<cairn::pipe::Shape<128, 128, 1, 4, 4>>();
   if(failures) {
     std::printf("pipe: %d failures\n", failures);
     return 1;

@@ -14,6 +14,7 @@
 
 from __future__ import annotations
 
+import ctypes as C
 import sys
 
 import numpy as np
@@ -74,13 +75,27 @@ def test_the_reference_device_shapes_equal_the_host_loop_bit_for_bit(name):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, m, n, k)
 
 
+def fits(info, m, n, k) -> bool:
+    """Whether the kernel `info` names can run an m x n x k problem in its layout (a selector question, no GPU)."""
+    ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
+    d = L.desc(t, L.I32 if t == L.I8 else L.F32, m, n, k, 1 << 20, 1 << 20, 1 << 20, trans_a=ta, trans_b=tb,
+               kernel=info["id"])  # fmt: skip
+    return L.load().cairn_gemm_select(C.byref(d), None) == L.OK
+
+
 def test_the_tile_simulator_shapes_equal_the_host_loop_for_every_kernel():
-    """Every tiled kernel (each layout, tile and operand size) on shapes with tails, exact data."""
+    """Every tiled kernel (each layout, tile and operand size) on shapes with tails, exact data. A kernel the selector
+    refuses for a shape (the one-wave-a-SIMD kernel needs long enough rows) skips it, but runs at least two."""
     for info in L.kernels():
-        if info["family"] not in ("mfma", "pipe"):
+        if info["family"] not in ("mfma", "pipe", "wave"):
             continue
         ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
-        for m, n, k in [(16, 16, 16), (info["tile_m"] + 16, info["tile_n"] + 32, 200), (272, 144, 72)]:
+        shapes = [(16, 16, 16), (info["tile_m"] + 16, info["tile_n"] + 32, 200), (272, 144, 72), (264, 264, 104),
+                  (288, 272, 96)]
+        shapes = [(m, n, (k + 15) // 16 * 16 if t == L.I8 else k) for m, n, k in shapes]
+        shapes = [s for s in shapes if fits(info, *s)]
+        assert len(shapes) >= 2, info["name"]
+        for m, n, k in shapes:
             if t == L.I8:
                 k = (k + 15) // 16 * 16
                 av = (H.tile_values(m * k, 7 + m) * 16).astype(np.int8)
@@ -99,6 +114,48 @@ def test_the_tile_simulator_shapes_equal_the_host_loop_for_every_kernel():
                 exact, _ = H.gemm_f64(t, m, n, k, a, b, trans_a=ta, trans_b=tb)
                 assert np.array_equal(got, (c0.astype(np.float64) + exact).astype(np.float32)), (info["name"], m, n, k)
             assert ch["kernel"] == info["id"]
+
+
+def test_every_ring_kernel_rounds_its_own_f32_result_to_bf16():
+    """The plain bf16 output (no epilogue) of each LDS-ring kernel is the nearest-even rounding of what the same
+    kernel computes in f32: the fast store path and the general one agree bit for bit."""
+    rng = np.random.default_rng(77)
+    for info in L.kernels():
+        if info["family"] not in ("pipe", "wave") or info["ab_type"] == L.I8:
+            continue
+        ta, tb = info["trans_a"], info["trans_b"]
+        m, n, k = info["tile_m"] + 40, info["tile_n"] + 24, 136
+        a = H.normal_bf16(rng, (k, m) if ta else (m, k), 1.0)
+        b = H.normal_bf16(rng, (n, k) if tb else (k, n), 1.0)
+        f32, _ = run_gemm(L.BF16, L.F32, m, n, k, a, b, trans_a=ta, trans_b=tb, kernel=info["id"])
+        b16, _ = run_gemm(L.BF16, L.BF16, m, n, k, a, b, trans_a=ta, trans_b=tb, kernel=info["id"])
+        assert np.array_equal(b16, H.bf16_from_f32(f32)), info["name"]
+
+
+@pytest.mark.parametrize("name", ["cairn_pipe_bf16_nn_256x256", "cairn_wave_bf16_nn_256x256"])
+def test_bf16_outputs_round_ties_to_even_keep_subnormals_and_overflow(name):
+    """Outputs exact in f32 that sit on bf16 rounding ties: near 1 (c = b0 +- 2^-8), among the subnormals
+    (c = 2^-127 b0, spacing 2^-133 against f32's 2^-149) and at the top (c = 2^127 (b0 + 2^-8), whose last tie rounds
+    to infinity). The bf16 output must be the f32 output narrowed (nearest even, the reference's narrow<bf16>)."""
+    m, n, k = 256, 256, 32
+    rows = np.arange(m) % 4
+    a = np.zeros((m, k), dtype=np.float64)
+    a[:, 0] = np.select([rows == 0, rows == 1, rows == 2, rows == 3], [1.0, 1.0, 2.0**-127, 2.0**127])
+    a[:, 1] = np.select([rows == 0, rows == 1, rows == 2, rows == 3], [2.0**-8, -(2.0**-8), 0.0, 2.0**119])
+    b = np.zeros((k, n), dtype=np.float64)
+    b[0, :] = 1.0 + (np.arange(n) % 128) / 128.0
+    b[1, :] = 1.0
+    a16, b16 = H.encode(L.BF16, a.ravel()).reshape(m, k), H.encode(L.BF16, b.ravel()).reshape(k, n)
+    assert np.array_equal(H.values(L.BF16, a16), a) and np.array_equal(H.values(L.BF16, b16), b)  # exact operands
+    kernel = L.kernel_named(name)
+    f32, ch = run_gemm(L.BF16, L.F32, m, n, k, a16, b16, kernel=kernel)
+    assert ch["name"] == name
+    exact = a @ b
+    assert np.array_equal(f32.astype(np.float64), exact)  # every output exact in f32
+    out, _ = run_gemm(L.BF16, L.BF16, m, n, k, a16, b16, kernel=kernel)
+    assert np.array_equal(out, H.bf16_from_f32(f32))
+    assert np.isinf(H.f32_from_bf16(out[3::4, 127])).all()  # 2^127 (2 - 2^-7 + 2^-8) rounds up to infinity
+    assert (H.f32_from_bf16(out[2::4, :]) <= 2.0**-126).all()  # the subnormal rows reach at most the least normal
 
 
 # ------------------------------------------------------------------ random operands: the contract
@@ -122,7 +179,7 @@ def test_random_operands_keep_the_contract_on_every_layout(fmt, trans_a, trans_b
         exact, mag = H.exact_product(A, B)
         c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
         got, ch = run_gemm(fmt, L.F32, m, n, k, a, b, c0, trans_a=trans_a, trans_b=trans_b, accumulate=True)
-        assert ch["family"] in ("mfma", "pipe")
+        assert ch["family"] in ("mfma", "pipe", "wave")
         assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
         # bf16 output: the contract plus half an ulp of the output format.
         got16, _ = run_gemm(fmt, L.BF16, m, n, k, a, b, trans_a=trans_a, trans_b=trans_b)

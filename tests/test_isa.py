@@ -1,0 +1,72 @@
+"""What the one-wave-a-SIMD kernel (cairn_amd/csrc/gemm_wave.hip) needs of the compiler, checked on its gfx950
+assembly: M0 holds the LDS base of a group of loads and each load picks its KiB by immediate offset, so between a write
+of M0 and the loads of its group nothing may write M0 again. The kernel writes M0 in inline assembly the compiler
+cannot see into; this test reads what the compiler emitted and holds it to that. No GPU is used: hipcc cross-compiles.
+"""
+
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-S", "--cuda-device-only", "-ffp-contract=off",
+         "-fno-fast-math", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]  # fmt: skip
+
+
+@pytest.fixture(scope="module")
+def assembly(tmp_path_factory) -> str:
+    if not shutil.which("hipcc"):
+        pytest.skip("hipcc is not installed")
+    out = tmp_path_factory.mktemp("isa") / "wave.s"
+    subprocess.run(["hipcc", *FLAGS, str(ROOT / "cairn_amd" / "csrc" / "gemm_wave.hip"), "-o", str(out)], check=True,
+                   capture_output=True, timeout=600)  # fmt: skip
+    return out.read_text()
+
+
+def kernels(asm: str) -> dict[str, list[str]]:
+    found = {}
+    for m in re.finditer(r"^(_ZN5cairn4gemm9wave_gemm\S*):", asm, re.M):
+        body = asm[m.end():asm.index(".Lfunc_end", m.end())]
+        found[m.group(1)] = [line.split(";")[0].strip() for line in body.splitlines() if line.strip()]
+    return found
+
+
+def test_every_lds_load_group_starts_with_its_own_base(assembly):
+    ks = kernels(assembly)
+    assert len(ks) >= 6
+    for name, lines in ks.items():
+        groups, current = [], None
+        for line in lines:
+            if "m0" in line:
+                assert re.fullmatch(r"s_mov_b32 m0, s\d+", line), (name, line)  # only the kernel's own writes
+                current = []
+                groups.append(current)
+            elif re.match(r"buffer_load_dwordx4 .* lds$", line):
+                assert current is not None, (name, "an LDS load before any base", line)
+                offset = re.search(r"offset:(0x[0-9a-f]+|\d+)", line)
+                current.append(int(offset.group(1), 0) if offset else 0)
+        assert groups, name
+        for g in groups:
+            assert g == [1024 * u for u in range(len(g))] and 1 <= len(g) <= 4, (name, g)
+
+
+def test_the_main_loop_writes_m0_twice_per_stage(assembly):
+    for name, lines in kernels(assembly).items():
+        loops = []
+        for i, line in enumerate(lines):
+            if re.match(r"s_cbranch_scc[01] (\.LBB\S+)", line):
+                target = line.split()[-1]
+                start = lines.index(target + ":")
+                if start < i and any("s_barrier" in x for x in lines[start:i]):
+                    loops.append(lines[start:i])
+        assert len(loops) == 1, name
+        loop = loops[0]
+        assert sum("m0" in x for x in loop) == 2, name
+        assert sum(x.startswith("v_mfma") for x in loop) == 32, name
+        assert sum(x == "s_barrier" for x in loop) == 1, name
+        assert not any(x.startswith(("scratch_", "buffer_store")) for x in loop), name  # no spills in the loop
