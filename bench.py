@@ -140,7 +140,7 @@ def bench_skinny(stream, steps, warmup) -> dict:
     return out
 
 
-def bench_mlp(stream, steps, warmup) -> dict:
+def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
     rng = np.random.default_rng(3)
     M, K, N = 8192, 4096, 11008
     x = hip.Buffer.of(bf16(rng.normal(0, 0.02, (M, K)).astype(np.float32)))
@@ -151,6 +151,9 @@ def bench_mlp(stream, steps, warmup) -> dict:
     fwd = L.desc(L.BF16, L.BF16, M, N, K, x.ptr, w.ptr, y.ptr, bias=bias.ptr, bias_type=L.BF16, act=L.ACT_GELU)
     bwd_x = L.desc(L.BF16, L.BF16, M, K, N, dy.ptr, w.ptr, dx.ptr, trans_b=True)  # dX = dY W^T (NT)
     bwd_w = L.desc(L.BF16, L.BF16, K, N, M, x.ptr, dy.ptr, dw.ptr, trans_a=True)  # dW = X^T dY (TN)
+    if family:
+        for d, lay in ((fwd, "nn"), (bwd_x, "nt"), (bwd_w, "tn")):
+            d.kernel = L.kernel_named(f"cairn_{family}_bf16_{lay}_256x256")
     out = {}
     flops = 2.0 * M * K * N
     for name, d in (("fwd", fwd), ("dx", bwd_x), ("dw", bwd_w)):
@@ -319,7 +322,7 @@ def main() -> int:
     if args.only in ("skinny", "all"):
         record["skinny"] = bench_skinny(stream, args.steps, args.warmup)
     if args.only in ("mlp", "all"):
-        record["mlp"] = bench_mlp(stream, args.steps, args.warmup)
+        record["mlp"] = bench_mlp(stream, args.steps, args.warmup, args.family)
     record["device"] = dev
     if not args.no_cpu:
         record["cpu_baseline"] = cpu_baseline()

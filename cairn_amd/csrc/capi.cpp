@@ -176,7 +176,7 @@ int resident(const Kernel& k) {
 double shape_rate(const Kernel& k) {
   const int area = k.bm * k.bn;
   if(k.family == PIPE) return area >= 256 * 256 ? 2.0 : (area >= 256 * 128 ? 1.8 : 1.5);
-  if(k.family == WAVE) return area >= 256 * 256 ? 1.9 : (area >= 256 * 128 ? 1.7 : 1.4);
+  if(k.family == WAVE) return area >= 256 * 256 ? 2.2 : (area >= 256 * 128 ? 1.9 : 1.6);
   if(area >= 256 * 256) return 1.0;
   if(area >= 256 * 128) return 0.92;
   return 0.78;

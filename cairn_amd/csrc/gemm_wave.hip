@@ -30,6 +30,7 @@
 // No atomics: the result's bits do not depend on timing.
 #include <hip/hip_runtime.h>
 #include <utility>
+#include "epilogue.hpp"
 #include "kernels.hpp"
 #include "mfma.hpp"
 #include "pipe.hpp"
@@ -55,7 +56,7 @@ __device__ __forceinline__ void fenced_barrier() {
   fence();
 }
 
-template<class Sh, int OP, bool TA, bool TB>
+template<class Sh, int OP, bool TA, bool TB, bool RAW>
 __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   static_assert(Sh::WAVES == 4, "one wave a SIMD");
   using M = Mfma<OP>;
@@ -218,22 +219,14 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
     }
     return;
   }
-#pragma unroll
-  for(int i = 0; i < FM; ++i) {
-    const int m = row0 + wr + 32 * i + cairn::tile::acc_m(lane);
-#pragma unroll
-    for(int j = 0; j < FN; ++j)
-#pragma unroll
-      for(int q = 0; q < 4; ++q) {
-        const int n = col0 + wc + 32 * j + cairn::tile::acc_n(lane, q);
-        if(m < p.m && n < p.n) store_quad(p, m, n, acc[i][j], q);
-      }
-  }
+  finish<RAW>(p, acc, row0 + wr, col0 + wc, lane);
 }
 
 template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave(const Params& p, hipStream_t s) {
   const unsigned grid = unsigned(p.tiles_m) * unsigned(p.tiles_n);
-  hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB>), dim3(grid), dim3(256), 0, s, p);
+  if(OP == OP_I8 && p.c_type == CAIRN_TYPE_I32)
+    hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB, OP == OP_I8>), dim3(grid), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB, false>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
