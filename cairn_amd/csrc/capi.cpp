@@ -22,6 +22,7 @@ using Launcher = hipError_t (*)(const Params&, hipStream_t);
 #undef CAIRN_WAVE_INSTANCE
 hipError_t cairn_generic(const Params&, hipStream_t);
 hipError_t cairn_skinny(const Params&, hipStream_t, int split);
+int cairn_skinny_width(int n);
 
 namespace {
 
@@ -45,7 +46,7 @@ struct Kernel {
 #define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, WAVE, OP, TA, TB, BM, BN, #NAME, STAGES},
 const Kernel TABLE[] = {
     {nullptr, GENERIC, -1, false, false, 64, 64, "cairn_generic_64x64", 1},
-    {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 32, "cairn_skinny_bf16_nt", 0},
+    {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 64, "cairn_skinny_bf16_nt", 0},
 #include "instances.inc"
 #include "pipe_instances.inc"
 #include "wave_instances.inc"
@@ -163,7 +164,7 @@ bool skinny_fits(const cairn_gemm_desc& d) {
 int lds_bytes(const Kernel& k) {
   if(ring(k)) return k.stages * (k.bm + k.bn) * 64;
   if(k.family == MFMA) return 2 * (k.bm + k.bn) * 128;
-  return k.family == GENERIC ? 4096 : 8192;
+  return k.family == GENERIC ? 4096 : 16384;  // skinny: four waves' partial sums
 }
 int resident(const Kernel& k) {
   if(k.family != MFMA && !ring(k)) return 8;
@@ -197,9 +198,10 @@ struct Estimate {
 Estimate estimate(const cairn_gemm_desc& d, const Kernel& k) {
   Estimate e{};
   if(k.family == SKINNY) {
-    const std::uint64_t blocks = (d.n + k.bn - 1) / k.bn;
+    const std::uint64_t width = std::uint64_t(cairn_skinny_width(int(d.n)));
+    const std::uint64_t blocks = (d.n + width - 1) / width;
     e.workgroups = blocks;
-    e.waves = double(blocks) / (CUS * 8.0);
+    e.waves = double(blocks) / CUS;  // one workgroup of four waves a CU
     e.efficiency = 1.0;
     e.cost = 1.0;
     return e;

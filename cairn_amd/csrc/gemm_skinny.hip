@@ -1,12 +1,16 @@
 // The skinny GEMM: m <= 16 rows of a (a decode step's tokens) against b stored n x k, K-contiguous (a weight matrix
 // as a linear layer keeps it), bf16 in, f32 accumulate. At m <= 16 the work is 2 m flops per b element, far below
-// the ridge of the roofline, so the kernel is built around streaming b from HBM once: every b byte is read by
-// exactly one 16-byte load, 8 columns' worth of loads in flight per lane, and the matrix cores do the arithmetic
-// (v_mfma_f32_16x16x32_bf16, its 16 rows holding a's m rows and zeros) so the vector ALUs never bound it.
+// the ridge of the roofline, so the kernel is built around streaming b from HBM once, evenly over the CUs: every b
+// byte is read by exactly one 16-byte load, and the matrix cores do the arithmetic (v_mfma_f32_16x16x32_bf16, its 16
+// rows holding a's m rows and zeros), so the vector ALUs never bound it.
 //
-// A workgroup of SPLIT waves owns 16 * GROUPS columns; each wave walks its own contiguous share of k for all of
-// them, and the waves' partial sums meet in LDS, added in wave order, so two runs give the same bits. The reference
-// has no decode path: its one tiling runs a 1 x n x k call as 64 x 64 tiles (src/cairn/runtime/cairn_tensor.hpp:206-221).
+// The columns are dealt out in equal ranges of `width` (a multiple of 8, at most 16 * GROUPS), one range a
+// workgroup, so that at n = 256 width every CU streams the same bytes (n = 14336: 56 columns a CU, 3.5 MFMA column
+// blocks, the last half masked). In a workgroup WAVES waves each walk their own contiguous share of k for all of its
+// columns, DEPTH k-steps of loads kept in flight in a ring of registers (deeper rings and more waves measured
+// slower: a k-step reads half of each 128-byte line, and the second half should find the first's line in L2); the waves' partial sums meet in LDS and are
+// added in wave order, so two runs give the same bits. The reference has no decode path: its one tiling runs a
+// 1 x n x k call as 64 x 64 tiles (src/cairn/runtime/cairn_tensor.hpp:206-221).
 #include <hip/hip_runtime.h>
 #include "kernels.hpp"
 
@@ -22,13 +26,16 @@ __device__ inline __amdgpu_buffer_rsrc_t span(const void* base, std::int64_t byt
 }
 constexpr int NOWHERE = 0x7fffffff;
 
-template<int GROUPS, int SPLIT, int UNROLL> __global__ void __launch_bounds__(64 * SPLIT) skinny_gemm(Params p) {
-  __shared__ f32x4 partial[SPLIT][GROUPS][64];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int n0 = int(blockIdx.x) * 16 * GROUPS;
-  const int row = lane & 15, piece = lane >> 4;  // MFMA operand: row (of a, or column of b) and 8-element k piece
+template<int GROUPS, int WAVES, int DEPTH>
+__global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
+  __shared__ f32x4 partial[WAVES][GROUPS][64];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the k loop below is a scalar loop
+  const int n0 = int(blockIdx.x) * width;
+  const int end = n0 + width < p.n ? n0 + width : p.n;  // this workgroup's columns: [n0, end)
+  const int row = lane & 15, piece = lane >> 4;         // MFMA operand: row (of a, or column of b), 8-element k piece
 
-  // b's rows n0 .. n0 + 16 * GROUPS, from their first element; a whole.
+  // b's rows n0 .., from their first element; a whole.
   const char* bp = static_cast<const char*>(p.b) + std::int64_t(n0) * p.ldb * 2;
   const std::int64_t bbytes = (std::int64_t(p.n - 1) * p.ldb + p.k) * 2 - std::int64_t(n0) * p.ldb * 2;
   const __amdgpu_buffer_rsrc_t rb = span(bp, bbytes);
@@ -36,36 +43,56 @@ template<int GROUPS, int SPLIT, int UNROLL> __global__ void __launch_bounds__(64
   int boff[GROUPS];
 #pragma unroll
   for(int g = 0; g < GROUPS; ++g)
-    boff[g] = n0 + 16 * g + row < p.n ? int((16 * g + row) * p.ldb * 2) + 16 * piece : NOWHERE;
+    boff[g] = n0 + 16 * g + row < end ? int((16 * g + row) * p.ldb * 2) + 16 * piece : NOWHERE;
   const int aoff = row < p.m ? int(row * p.lda * 2) + 16 * piece : NOWHERE;
 
   // This wave's k-steps of 32: [first, last).
   const int steps = (p.k + 31) / 32;
-  const int first = int(std::int64_t(steps) * wave / SPLIT), last = int(std::int64_t(steps) * (wave + 1) / SPLIT);
+  const int first = int(std::int64_t(steps) * wave / WAVES), last = int(std::int64_t(steps) * (wave + 1) / WAVES);
   f32x4 acc[GROUPS];
 #pragma unroll
   for(int g = 0; g < GROUPS; ++g) acc[g] = f32x4{0, 0, 0, 0};
 
-  auto fetch = [&](int step, w32x4& xa, w32x4 (&xb)[GROUPS]) {
-    const int k = step * 32 + 8 * piece;  // this lane's 8 elements of k
-    const bool inside = step < last && k < p.k;
-    xa = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, inside && aoff != NOWHERE ? aoff + step * 64 : NOWHERE, 0, 0));
+  // k-steps of 32 whole (every piece inside k) need no per-lane test; only a last partial step does.
+  const int whole = p.k / 32;
+  w32x4 xa[DEPTH], xb[DEPTH][GROUPS];
+  auto fetch = [&](int step, int slot) {
+    int oa = aoff + step * 64;
+    int ob[GROUPS];
+#pragma unroll
+    for(int g = 0; g < GROUPS; ++g) ob[g] = boff[g] + step * 64;
+    if(step >= whole) {  // uniform: the partial last step, or a step of the ring past this wave's share
+      const bool inside = step < last && step * 32 + 8 * piece < p.k;
+      oa = inside && aoff != NOWHERE ? oa : NOWHERE;
+#pragma unroll
+      for(int g = 0; g < GROUPS; ++g) ob[g] = inside && boff[g] != NOWHERE ? ob[g] : NOWHERE;
+    }
+    // NOWHERE + step * 64 stays past every buffer's range (an unsigned offset below 2^32), so a masked lane reads 0.
+    xa[slot] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, oa, 0, 0));
+#pragma unroll
+    for(int g = 0; g < GROUPS; ++g)  // (nontemporal loads measured slower here: a step reads half of each line)
+      xb[slot][g] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, ob[g], 0, 0));
+  };
+  auto use = [&](int slot) {
 #pragma unroll
     for(int g = 0; g < GROUPS; ++g)
-      xb[g] = __builtin_bit_cast(
-          w32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, inside && boff[g] != NOWHERE ? boff[g] + step * 64 : NOWHERE, 0, 0));
+      acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[slot]),
+                                                       __builtin_bit_cast(bf16x8, xb[slot][g]), acc[g], 0, 0, 0);
   };
-  for(int s = first; s < last; s += UNROLL) {
-    w32x4 xa[UNROLL], xb[UNROLL][GROUPS];
+  // A ring of DEPTH steps: step s lives in slot s % DEPTH; using it frees the slot for step s + DEPTH, whose loads
+  // go out at once, so DEPTH - 1 steps stay in flight while one is used (scheduling fences keep the compiler from
+  // gathering the uses, which would wait for every load). Steps of the ring past `last` load nothing and are not used.
 #pragma unroll
-    for(int u = 0; u < UNROLL; ++u) fetch(s + u, xa[u], xb[u]);
+  for(int d = 0; d < DEPTH; ++d) fetch(first + d, d);
+  for(int s = first; s < last; s += DEPTH) {
 #pragma unroll
-    for(int u = 0; u < UNROLL; ++u)
-#pragma unroll
-      for(int g = 0; g < GROUPS; ++g)
-        acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[u]),
-                                                         __builtin_bit_cast(bf16x8, xb[u][g]), acc[g], 0, 0, 0);
+    for(int d = 0; d < DEPTH; ++d) {
+      __builtin_amdgcn_sched_barrier(0);
+      if(s + d < last) use(d);
+      fetch(s + DEPTH + d, d);
+    }
   }
+  __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
   for(int g = 0; g < GROUPS; ++g) partial[wave][g][lane] = acc[g];
@@ -76,9 +103,9 @@ template<int GROUPS, int SPLIT, int UNROLL> __global__ void __launch_bounds__(64
   for(int g = 0; g < GROUPS; ++g) {
     f32x4 sum = partial[0][g][lane];
 #pragma unroll
-    for(int w = 1; w < SPLIT; ++w) sum = sum + partial[w][g][lane];
+    for(int w = 1; w < WAVES; ++w) sum = sum + partial[w][g][lane];
     const int n = n0 + 16 * g + (lane & 15);
-    if(n >= p.n) continue;
+    if(n >= end) continue;
 #pragma unroll
     for(int r = 0; r < 4; ++r) {
       const int m = 4 * (lane >> 4) + r;
@@ -98,10 +125,18 @@ template<int GROUPS, int SPLIT, int UNROLL> __global__ void __launch_bounds__(64
 
 }  // namespace cairn::gemm
 
-// 32 columns and four waves a workgroup: n / 32 workgroups, each wave a quarter of k.
+// The width of a workgroup's columns for n: n spread evenly over the 256 CUs, in multiples of 8, from 8 up to the
+// 64 columns a workgroup holds (past 256 x 64 columns the workgroups simply grow in number).
+int cairn_skinny_width(int n) {
+  const int even = (n + 255) / 256;
+  const int w = (even + 7) / 8 * 8;
+  return w < 8 ? 8 : (w > 64 ? 64 : w);
+}
+
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
-  constexpr int GROUPS = 2, SPLIT = 4, UNROLL = 4;
-  const dim3 grid(unsigned((p.n + 16 * GROUPS - 1) / (16 * GROUPS)));
-  hipLaunchKernelGGL((cairn::gemm::skinny_gemm<GROUPS, SPLIT, UNROLL>), grid, dim3(64 * SPLIT), 0, s, p);
+  constexpr int GROUPS = 4, WAVES = 4, DEPTH = 4;  // measured best of 4 / 8 waves, depth 2 / 4 / 8
+  const int width = cairn_skinny_width(p.n);
+  const dim3 grid(unsigned((p.n + width - 1) / width));
+  hipLaunchKernelGGL((cairn::gemm::skinny_gemm<GROUPS, WAVES, DEPTH>), grid, dim3(64 * WAVES), 0, s, p, width);
   return hipGetLastError();
 }
