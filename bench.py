@@ -195,7 +195,7 @@ def bench_traffic(stream, launches: int = 3, family: str | None = None) -> dict:
     return {"kernel": name, "launches": launches, "copy_bytes": COPY_BYTES}
 
 
-TRAFFIC = ROOT / "profiles" / "traffic_pipe_bf16_4096.md"
+TRAFFIC = ROOT / "profiles" / "traffic_wave_bf16_4096.md"
 
 
 def measured_traffic(kernel: str) -> dict | None:
