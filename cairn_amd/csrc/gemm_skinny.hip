@@ -7,11 +7,14 @@
 // The columns are dealt out in equal ranges of `width` (a multiple of 8, at most 16 * GROUPS), one range a
 // workgroup, so that at n = 256 width every CU streams the same bytes (n = 14336: 56 columns a CU, 3.5 MFMA column
 // blocks, the last half masked). In a workgroup WAVES waves each walk their own contiguous share of k for all of its
-// columns, DEPTH k-steps of loads kept in flight in a ring of registers (deeper rings and more waves measured
-// slower: a k-step reads half of each 128-byte line, and the second half should find the first's line in L2); the waves' partial sums meet in LDS and are
-// added in wave order, so two runs give the same bits. The reference has no decode path: its one tiling runs a
-// 1 x n x k call as 64 x 64 tiles (src/cairn/runtime/cairn_tensor.hpp:206-221).
+// columns, in chunks of CH k-steps of 32: a's chunk is held in registers, and b's column blocks are loaded one at a
+// time, each lane CH consecutive 16-byte pieces of its row (16 rows of CH * 64 bytes together), the next block's
+// loads in flight while the current block's MFMAs run. Asking for each row's bytes together keeps DRAM pages open:
+// the same loads spread over time, 64 bytes of a row at a time, measured a fifth slower. The waves' partial sums meet
+// in LDS and are added in wave order, so two runs give the same bits. The reference has no decode path: its one
+// tiling runs a 1 x n x k call as 64 x 64 tiles (src/cairn/runtime/cairn_tensor.hpp:206-221).
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include "kernels.hpp"
 
 namespace cairn::gemm {
@@ -26,7 +29,7 @@ __device__ inline __amdgpu_buffer_rsrc_t span(const void* base, std::int64_t byt
 }
 constexpr int NOWHERE = 0x7fffffff;
 
-template<int GROUPS, int WAVES, int DEPTH>
+template<int GROUPS, int WAVES, int CH>
 __global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
   __shared__ f32x4 partial[WAVES][GROUPS][64];
   const int t = threadIdx.x, lane = t & 63;
@@ -46,53 +49,58 @@ __global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
     boff[g] = n0 + 16 * g + row < end ? int((16 * g + row) * p.ldb * 2) + 16 * piece : NOWHERE;
   const int aoff = row < p.m ? int(row * p.lda * 2) + 16 * piece : NOWHERE;
 
-  // This wave's k-steps of 32: [first, last).
-  const int steps = (p.k + 31) / 32;
+  // This wave's k-steps of 32: [first, last). Steps whole in k (below `whole`) need no per-lane test.
+  const int steps = (p.k + 31) / 32, whole = p.k / 32;
   const int first = int(std::int64_t(steps) * wave / WAVES), last = int(std::int64_t(steps) * (wave + 1) / WAVES);
   f32x4 acc[GROUPS];
 #pragma unroll
   for(int g = 0; g < GROUPS; ++g) acc[g] = f32x4{0, 0, 0, 0};
 
-  // k-steps of 32 whole (every piece inside k) need no per-lane test; only a last partial step does.
-  const int whole = p.k / 32;
-  w32x4 xa[DEPTH], xb[DEPTH][GROUPS];
-  auto fetch = [&](int step, int slot) {
-    int oa = aoff + step * 64;
-    int ob[GROUPS];
-#pragma unroll
-    for(int g = 0; g < GROUPS; ++g) ob[g] = boff[g] + step * 64;
-    if(step >= whole) {  // uniform: the partial last step, or a step of the ring past this wave's share
-      const bool inside = step < last && step * 32 + 8 * piece < p.k;
-      oa = inside && aoff != NOWHERE ? oa : NOWHERE;
-#pragma unroll
-      for(int g = 0; g < GROUPS; ++g) ob[g] = inside && boff[g] != NOWHERE ? ob[g] : NOWHERE;
-    }
-    // NOWHERE + step * 64 stays past every buffer's range (an unsigned offset below 2^32), so a masked lane reads 0.
-    xa[slot] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, oa, 0, 0));
-#pragma unroll
-    for(int g = 0; g < GROUPS; ++g)  // (nontemporal loads measured slower here: a step reads half of each line)
-      xb[slot][g] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, ob[g], 0, 0));
+  // The offset of a lane's 16 bytes at `step`, or one past every range (the load reads zeros: a masked row or
+  // column, a step past this wave's share, or k past its end). NOWHERE + step * 64 stays above every buffer's range.
+  auto offset = [&](int base, int step) {
+    int o = base + step * 64;
+    if(step >= last) o = NOWHERE;  // uniform: the next wave's step, or past k
+    else if(step >= whole)         // uniform: the partial last step of k
+      o = step * 32 + 8 * piece < p.k && base != NOWHERE ? o : NOWHERE;
+    return o;
   };
-  auto use = [&](int slot) {
+  w32x4 xa[CH], xb[2][CH];
+  // A chunk of CH steps wholly inside this wave's share and inside k (every chunk but perhaps a wave's last) loads
+  // with plain offsets; the other takes `offset`'s tests. CLEAN is a compile-time switch between the two copies.
+  auto chunk = [&](int s0, auto clean) {
+    constexpr bool CLEAN = decltype(clean)::value;
+    auto at = [&](int base, int step) { return CLEAN ? (base == NOWHERE ? NOWHERE : base + step * 64) : offset(base, step); };
+    auto load_b = [&](int g, int buf) {
 #pragma unroll
-    for(int g = 0; g < GROUPS; ++g)
-      acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[slot]),
-                                                       __builtin_bit_cast(bf16x8, xb[slot][g]), acc[g], 0, 0, 0);
-  };
-  // A ring of DEPTH steps: step s lives in slot s % DEPTH; using it frees the slot for step s + DEPTH, whose loads
-  // go out at once, so DEPTH - 1 steps stay in flight while one is used (scheduling fences keep the compiler from
-  // gathering the uses, which would wait for every load). Steps of the ring past `last` load nothing and are not used.
+      for(int u = 0; u < CH; ++u)
+        xb[buf][u] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, at(boff[g], s0 + u), 0, 0));
+    };
+    // Zeros (steps past the share read nothing) add nothing: the accumulators start at +0 and stay off -0.
+    auto mfma = [&](int g, int buf) {
 #pragma unroll
-  for(int d = 0; d < DEPTH; ++d) fetch(first + d, d);
-  for(int s = first; s < last; s += DEPTH) {
+      for(int u = 0; u < CH; ++u)
+        acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[u]),
+                                                         __builtin_bit_cast(bf16x8, xb[buf][u]), acc[g], 0, 0, 0);
+    };
 #pragma unroll
-    for(int d = 0; d < DEPTH; ++d) {
+    for(int u = 0; u < CH; ++u)
+      xa[u] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, at(aoff, s0 + u), 0, 0));
+    load_b(0, 0);
+#pragma unroll
+    for(int g = 0; g < GROUPS; ++g) {
+      // Scheduling fences keep the next block's loads ahead of this block's MFMAs, which wait only for their own.
       __builtin_amdgcn_sched_barrier(0);
-      if(s + d < last) use(d);
-      fetch(s + DEPTH + d, d);
+      if(g + 1 < GROUPS) load_b(g + 1, (g + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(g, g & 1);
     }
-  }
-  __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const int clean_end = last < whole ? last : whole;  // steps below this need no test
+  int s0 = first;
+  for(; s0 + CH <= clean_end; s0 += CH) chunk(s0, std::true_type{});
+  for(; s0 < last; s0 += CH) chunk(s0, std::false_type{});  // a short or partial last chunk
 
 #pragma unroll
   for(int g = 0; g < GROUPS; ++g) partial[wave][g][lane] = acc[g];
@@ -134,9 +142,9 @@ int cairn_skinny_width(int n) {
 }
 
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
-  constexpr int GROUPS = 4, WAVES = 4, DEPTH = 4;  // measured best of 4 / 8 waves, depth 2 / 4 / 8
+  constexpr int GROUPS = 4, WAVES = 4, CH = 8;  // measured best of 2 / 4 / 8 waves and chunks of 8 / 16 steps
   const int width = cairn_skinny_width(p.n);
   const dim3 grid(unsigned((p.n + width - 1) / width));
-  hipLaunchKernelGGL((cairn::gemm::skinny_gemm<GROUPS, WAVES, DEPTH>), grid, dim3(64 * WAVES), 0, s, p, width);
+  hipLaunchKernelGGL((cairn::gemm::skinny_gemm<GROUPS, WAVES, CH>), grid, dim3(64 * WAVES), 0, s, p, width);
   return hipGetLastError();
 }

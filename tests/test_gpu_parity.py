@@ -279,7 +279,8 @@ def test_skinny_decode_shapes_keep_the_contract(m):
     assert H.outside(v, exact, room) == 0
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 8, 8), (3, 100, 72), (16, 33, 4104), (7, 14336, 24)])
+@pytest.mark.parametrize("m,n,k", [(1, 8, 8), (3, 100, 72), (16, 33, 4104), (7, 14336, 24), (5, 200, 4160),
+                                   (2, 72, 1000)])
 def test_skinny_tails_keep_the_contract(m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = H.normal_bf16(rng, (m, k), 1.0)
