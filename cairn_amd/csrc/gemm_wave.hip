@@ -203,12 +203,38 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
       *reinterpret_cast<u32x2*>(c + (std::int64_t(m) * p.ldc + n) * 2) = w;
     };
     if(whole) {
+      // Through LDS, so that every store writes whole rows: the wave's WTM x WTN bf16 block goes into its own part
+      // of the ring (free once every wave has passed the barrier), 8 bytes a quad, then comes back 16 bytes a lane,
+      // a row of the block per 16 lanes. The 8-byte unit u of row r sits at unit u ^ (r % 32) of the row, which keeps
+      // both the writes (32 rows, one unit each) and the reads (16 units of one row) on distinct banks; a read of an
+      // odd row finds its two halves swapped.
+      static_assert(Sh::WTN * 2 == 256 && Sh::WTM * 256 * Sh::WAVES <= S * Sh::STAGE, "a row of the block is 256 bytes");
+      fenced_barrier();
+      char* mine = lds + wave * (Sh::WTM * 256);
+      const int h = lane >> 5;
 #pragma unroll
-      for(int i = 0; i < FM; ++i)
+      for(int i = 0; i < FM; ++i) {
+        const int r = 32 * i + (lane & 31);
 #pragma unroll
         for(int j = 0; j < FN; ++j)
 #pragma unroll
-          for(int q = 0; q < 4; ++q) quad(i, j, q, false);
+          for(int q = 0; q < 4; ++q) {
+            u32x2 w;
+            w[0] = narrow2_bf16(float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]));
+            w[1] = narrow2_bf16(float(acc[i][j][4 * q + 2]), float(acc[i][j][4 * q + 3]));
+            const int unit = (8 * j + 2 * q + h) ^ (r & 31);
+            *reinterpret_cast<u32x2*>(mine + r * 256 + unit * 8) = w;
+          }
+      }
+      const int cl = lane & 15;
+      char* out = c + (std::int64_t(row0 + wr) * p.ldc + col0 + wc) * 2 + 16 * cl;
+#pragma unroll
+      for(int s = 0; s < Sh::WTM / 4; ++s) {
+        const int r = 4 * s + (lane >> 4);
+        u32x4 v = *reinterpret_cast<const u32x4*>(mine + r * 256 + 16 * (cl ^ ((r & 31) >> 1)));
+        if(r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+        *reinterpret_cast<u32x4*>(out + std::int64_t(r) * p.ldc * 2) = v;
+      }
     } else {
 #pragma unroll
       for(int i = 0; i < FM; ++i)
