@@ -18,8 +18,10 @@ using Launcher = hipError_t (*)(const Params&, hipStream_t);
 #include "pipe_instances.inc"
 #undef CAIRN_PIPE_INSTANCE
 #define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
+#define CAIRN_WAVE8_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
 #include "wave_instances.inc"
 #undef CAIRN_WAVE_INSTANCE
+#undef CAIRN_WAVE8_INSTANCE
 hipError_t cairn_generic(const Params&, hipStream_t);
 hipError_t cairn_skinny(const Params&, hipStream_t, int split);
 int cairn_skinny_width(int n);
@@ -44,6 +46,7 @@ struct Kernel {
 #define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) {NAME, MFMA, OP, TA, TB, BM, BN, #NAME, 2},
 #define CAIRN_PIPE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, PIPE, OP, TA, TB, BM, BN, #NAME, STAGES},
 #define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, WAVE, OP, TA, TB, BM, BN, #NAME, STAGES},
+#define CAIRN_WAVE8_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, WAVE, OP, TA, TB, BM, BN, #NAME, STAGES},
 const Kernel TABLE[] = {
     {nullptr, GENERIC, -1, false, false, 64, 64, "cairn_generic_64x64", 1},
     {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 64, "cairn_skinny_bf16_nt", 0},
@@ -54,6 +57,7 @@ const Kernel TABLE[] = {
 #undef CAIRN_MFMA_INSTANCE
 #undef CAIRN_PIPE_INSTANCE
 #undef CAIRN_WAVE_INSTANCE
+#undef CAIRN_WAVE8_INSTANCE
 constexpr int COUNT = int(sizeof(TABLE) / sizeof(TABLE[0]));
 
 int op_of(int type) {
@@ -61,7 +65,9 @@ int op_of(int type) {
     case CAIRN_TYPE_BF16: return cairn::gemm::OP_BF16;
     case CAIRN_TYPE_F16: return cairn::gemm::OP_F16;
     case CAIRN_TYPE_I8: return cairn::gemm::OP_I8;
-    default: return -1;  // the 8-bit floats: the generic kernel widens them
+    case CAIRN_TYPE_F8E4M3: return cairn::gemm::OP_F8E4M3;  // the fp8 matrix core; the generic kernel widens them
+    case CAIRN_TYPE_F8E5M2: return cairn::gemm::OP_F8E5M2;  // where no tiled kernel fits
+    default: return -1;
   }
 }
 int element_size(int type) { return type == CAIRN_TYPE_BF16 || type == CAIRN_TYPE_F16 ? 2 : 1; }
@@ -187,7 +193,8 @@ double shape_rate(const Kernel& k) {
 int tile_k(const Kernel& k) {
   const int bytes = k.family == MFMA ? 128 : (ring(k) ? 64 : 32);
   if(k.family == SKINNY) return 32;
-  return k.op == cairn::gemm::OP_I8 ? bytes : bytes / 2;
+  const bool byte = k.op == cairn::gemm::OP_I8 || k.op == cairn::gemm::OP_F8E4M3 || k.op == cairn::gemm::OP_F8E5M2;
+  return byte ? bytes : bytes / 2;
 }
 
 struct Estimate {
@@ -286,10 +293,12 @@ int cairn_gemm_kernel_info(int32_t id, cairn_gemm_kernel* out) {
   const Kernel& k = TABLE[id - 1];
   std::memset(out, 0, sizeof(*out));
   out->id = id;
-  out->ab_type = k.op == cairn::gemm::OP_BF16 ? CAIRN_TYPE_BF16
-                 : k.op == cairn::gemm::OP_F16 ? CAIRN_TYPE_F16
-                 : k.op == cairn::gemm::OP_I8  ? CAIRN_TYPE_I8
-                                               : -1;
+  out->ab_type = k.op == cairn::gemm::OP_BF16     ? CAIRN_TYPE_BF16
+                 : k.op == cairn::gemm::OP_F16    ? CAIRN_TYPE_F16
+                 : k.op == cairn::gemm::OP_I8     ? CAIRN_TYPE_I8
+                 : k.op == cairn::gemm::OP_F8E4M3 ? CAIRN_TYPE_F8E4M3
+                 : k.op == cairn::gemm::OP_F8E5M2 ? CAIRN_TYPE_F8E5M2
+                                                  : -1;
   out->trans_a = k.ta;
   out->trans_b = k.tb;
   out->tile_m = k.bm;

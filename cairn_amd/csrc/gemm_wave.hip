@@ -248,6 +248,137 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   finish<RAW>(p, acc, row0 + wr, col0 + wc, lane);
 }
 
+// The 8-bit floats on the same ring: one v_mfma_f32_32x32x64_f8f6f4 covers a whole stage (64 bytes of k), so a
+// stage's fragments, both 16-byte k-steps of the int8 layout, are read during the previous stage's MFMAs, double-
+// buffered by stage. Iteration `it`:
+//   wait for this wave's loads of stage it + 1 and its own LDS reads; barrier;
+//   the 16 MFMAs of stage it, between them the fragment reads of stage it + 1 and the loads of stage it + STAGES
+//   into the buffer stage it used (every wave has stage it in registers once past the barrier).
+// The hazards are the ones of wave_gemm, ordered by the one barrier a stage.
+template<class Sh, int OP, bool TA, bool TB>
+__global__ void __launch_bounds__(256) wave8_gemm(Params p) {
+  static_assert(Sh::WAVES == 4 && Sh::ES == 1, "one wave a SIMD, 8-bit operands");
+  using M = Mfma<OP>;
+  using Acc = typename M::Acc;
+  constexpr bool AK = !TA, BKM = TB;
+  constexpr int S = Sh::STAGES, FM = Sh::FM, FN = Sh::FN, ES = Sh::ES;
+  constexpr int LOADS = Sh::LOADS_A + Sh::LOADS_B;
+  constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, STEP_READS = RA + RB, READS = 2 * STEP_READS;
+  static_assert(READS <= 32 && Sh::LOADS_A <= 4 && Sh::LOADS_B <= 4, "the interleave below");
+  __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  int wr, wc;
+  wave_origin<Sh>(wave, wr, wc);
+  int tm, tn;
+  cairn::tile::tile_of(int(blockIdx.x), p.tiles_m, p.tiles_n, p.group, tm, tn);
+  const int row0 = tm * Sh::BM, col0 = tn * Sh::BN;
+  const cairn::tile::Panel pa = cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES);
+  const cairn::tile::Panel pb = cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES);
+  const char* a = static_cast<const char*>(p.a) + pa.start;
+  const char* b = static_cast<const char*>(p.b) + pb.start;
+  const unsigned ring = lds_address(lds);
+
+  Dma dma;
+  Loader<Sh, Sh::BM, AK, Dma> la;
+  Loader<Sh, Sh::BN, BKM, Dma> lb;  // the host runs this kernel only where both loaders' imm_fits holds
+  la.setup(t, row0, p.m, p.lda);
+  lb.setup(t, col0, p.n, p.ldb);
+  const int T = (p.k + Sh::BK - 1) / Sh::BK;
+  using LA = Loader<Sh, Sh::BM, AK, Dma>;
+  using LB = Loader<Sh, Sh::BN, BKM, Dma>;
+  auto at_of = [&](int st) { return ring + unsigned((st % S) * Sh::STAGE); };
+  auto load_a = [&](const auto& r, int st, auto u) {
+    if constexpr(decltype(u)::value == 0) dma.set_base(LA::base(at_of(st), wave));
+    la.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  };
+  auto load_b = [&](const auto& r, int st, auto u) {
+    if constexpr(decltype(u)::value == 0) dma.set_base(LB::base(at_of(st) + Sh::A_BYTES, wave));
+    lb.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  };
+  auto stage_all = [&](int st) {
+    const auto ra = la.resource(dma, a, pa.bytes, p.lda, st);
+    unrolled<Sh::LOADS_A>([&](auto u) { load_a(ra, st, u); });
+    const auto rb = lb.resource(dma, b, pb.bytes, p.ldb, st);
+    unrolled<Sh::LOADS_B>([&](auto u) { load_b(rb, st, u); });
+  };
+
+  Acc acc[FM][FN];
+#pragma unroll
+  for(int i = 0; i < FM; ++i)
+#pragma unroll
+    for(int j = 0; j < FN; ++j) acc[i][j] = Acc{};
+  u32x4 xa[2][2][FM], xb[2][2][FN];  // [buffer][k-step of the stage][block]
+  // Read X of a stage's READS: k-step X / STEP_READS, then as wave_gemm orders a k-step's reads.
+  auto read = [&](auto buf, const char* stage, auto x) {
+    constexpr int BUF = decltype(buf)::value, X = decltype(x)::value % STEP_READS, s = decltype(x)::value / STEP_READS;
+    if constexpr(X < RA) {
+      if constexpr(AK) xa[BUF][s][X] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(wr + 32 * X, s, lane));
+      else {
+        const u32x2 h = transpose_half<ES>(stage + mnmajor_fragment<ES, Sh::BM>(wr + 32 * (X / 2), s, X % 2, lane));
+        xa[BUF][s][X / 2][2 * (X % 2)] = h[0];
+        xa[BUF][s][X / 2][2 * (X % 2) + 1] = h[1];
+      }
+    } else {
+      constexpr int Y = X - RA;
+      const char* bs = stage + Sh::A_BYTES;
+      if constexpr(BKM) xb[BUF][s][Y] = *reinterpret_cast<const u32x4*>(bs + kmajor_fragment(wc + 32 * Y, s, lane));
+      else {
+        const u32x2 h = transpose_half<ES>(bs + mnmajor_fragment<ES, Sh::BN>(wc + 32 * (Y / 2), s, Y % 2, lane));
+        xb[BUF][s][Y / 2][2 * (Y % 2)] = h[0];
+        xb[BUF][s][Y / 2][2 * (Y % 2) + 1] = h[1];
+      }
+    }
+  };
+  auto mfma = [&](auto buf, auto x) {
+    constexpr int BUF = decltype(buf)::value, I = decltype(x)::value / FN, J = decltype(x)::value % FN;
+    acc[I][J] = M::step(xb[BUF][0][J], xb[BUF][1][J], xa[BUF][0][I], xa[BUF][1][I], acc[I][J]);
+  };
+  auto stage_of = [&](int st) { return lds + (st % S) * Sh::STAGE; };
+
+  // Stages 0 .. S - 1 (every buffer starts free), then stage 0's fragments.
+  for(int st = 0; st < S; ++st) stage_all(st);
+  wait_loads<(S - 1) * LOADS>();
+  fenced_barrier();
+  unrolled<READS>([&](auto x) { read(std::integral_constant<int, 0>{}, stage_of(0), x); });
+
+  auto iteration = [&](int it, auto cur) {
+    constexpr int C = decltype(cur)::value, N = 1 - C;
+    const int sl = it + S;  // the stage whose loads this iteration issues, into stage it's buffer
+    const auto ra = la.resource(dma, a, pa.bytes, p.lda, sl);
+    const auto rb = lb.resource(dma, b, pb.bytes, p.ldb, sl);
+    const char* nxt = stage_of(it + 1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    wait_loads<(S - 2) * LOADS>();
+    fenced_barrier();
+    unrolled<FM * FN>([&](auto x) {
+      constexpr int X = decltype(x)::value;
+      mfma(std::integral_constant<int, C>{}, x);
+      fence();
+      if constexpr(2 * X < READS) read(std::integral_constant<int, N>{}, nxt, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(std::integral_constant<int, N>{}, nxt, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(X >= 4 && X < 4 + Sh::LOADS_A) load_a(ra, sl, std::integral_constant<int, X - 4>{});
+      if constexpr(X >= 8 && X < 8 + Sh::LOADS_B) load_b(rb, sl, std::integral_constant<int, X - 8>{});
+      fence();
+    });
+  };
+  int it = 0;
+  for(; it + 1 < T; it += 2) {
+    iteration(it, std::integral_constant<int, 0>{});
+    iteration(it + 1, std::integral_constant<int, 1>{});
+  }
+  if(it < T) iteration(it, std::integral_constant<int, 0>{});
+  wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
+  finish<false>(p, acc, row0 + wr, col0 + wc, lane);
+}
+
+template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave8(const Params& p, hipStream_t s) {
+  const unsigned grid = unsigned(p.tiles_m) * unsigned(p.tiles_n);
+  hipLaunchKernelGGL((wave8_gemm<Sh, OP, TA, TB>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
 template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave(const Params& p, hipStream_t s) {
   const unsigned grid = unsigned(p.tiles_m) * unsigned(p.tiles_n);
   if(OP == OP_I8 && p.c_type == CAIRN_TYPE_I32)
@@ -262,5 +393,9 @@ template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave(const Params
   hipError_t NAME(const cairn::gemm::Params& p, hipStream_t s) {                                                 \
     return cairn::gemm::launch_wave<                                                                              \
         cairn::pipe::Shape<BM, BN, (OP == cairn::gemm::OP_I8 ? 1 : 2), STAGES, 4>, OP, TA, TB>(p, s);           \
+  }
+#define CAIRN_WAVE8_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB)                                                     \
+  hipError_t NAME(const cairn::gemm::Params& p, hipStream_t s) {                                                 \
+    return cairn::gemm::launch_wave8<cairn::pipe::Shape<BM, BN, 1, STAGES, 4>, OP, TA, TB>(p, s);                \
   }
 #include "wave_instances.inc"

@@ -9,7 +9,7 @@
 namespace cairn::gemm {
 
 // The matrix-core operations the tiled kernels run on.
-enum Op { OP_BF16 = 0, OP_F16 = 1, OP_I8 = 2 };
+enum Op { OP_BF16 = 0, OP_F16 = 1, OP_I8 = 2, OP_F8E4M3 = 3, OP_F8E5M2 = 4 };
 
 // One launch. Matrices are the caller's: a is m x k (trans_a: stored k x m), b is k x n (trans_b: stored n x k), c
 // is m x n; ld* count elements between stored rows. Extents fit int32 (the host checks).

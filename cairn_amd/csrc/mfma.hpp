@@ -42,6 +42,23 @@ template<> struct Mfma<OP_I8> {
   }
 };
 
+// The 8-bit floats on v_mfma_f32_32x32x64_f8f6f4 (OCP E4M3 or E5M2 for both operands; the scaled builtin with zero
+// scale operands, which is the unscaled instruction): one step covers 64 bytes of k, each operand the two 16-byte
+// k-steps of the int8 layout side by side. The instruction pairs the operands' bytes position by position, so any
+// one order of k that both operands share gives the same sum.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+template<int FMT> struct Mfma8 {
+  using Acc = f32x16;
+  static constexpr int ES = 1;
+  __device__ static Acc step(u32x4 x0, u32x4 x1, u32x4 y0, u32x4 y1, Acc c) {
+    const i32x8 x = {int(x0[0]), int(x0[1]), int(x0[2]), int(x0[3]), int(x1[0]), int(x1[1]), int(x1[2]), int(x1[3])};
+    const i32x8 y = {int(y0[0]), int(y0[1]), int(y0[2]), int(y0[3]), int(y1[0]), int(y1[1]), int(y1[2]), int(y1[3])};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(x, y, c, FMT, FMT, 0, 0, 0, 0);
+  }
+};
+template<> struct Mfma<OP_F8E4M3> : Mfma8<0> {};
+template<> struct Mfma<OP_F8E5M2> : Mfma8<1> {};
+
 // Quad q of one 32 x 32 accumulator block is row m, columns n .. n+3 (tile.hpp, acc_m / acc_n): the epilogue of
 // those four outputs and their store, 16 bytes (f32, int32) or 8 (bf16, f16). The caller has checked m < p.m and
 // n < p.n; n is a multiple of 4 and p.n too, so all four columns exist.

@@ -92,7 +92,8 @@ def test_the_tile_simulator_shapes_equal_the_host_loop_for_every_kernel():
         ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
         shapes = [(16, 16, 16), (info["tile_m"] + 16, info["tile_n"] + 32, 200), (272, 144, 72), (264, 264, 104),
                   (288, 272, 96)]
-        shapes = [(m, n, (k + 15) // 16 * 16 if t == L.I8 else k) for m, n, k in shapes]
+        byte = t in (L.I8, L.F8E4M3, L.F8E5M2)
+        shapes = [(m, n, (k + 15) // 16 * 16 if byte else k) for m, n, k in shapes]
         shapes = [s for s in shapes if fits(info, *s)]
         assert len(shapes) >= 2, info["name"]
         for m, n, k in shapes:
@@ -121,7 +122,7 @@ def test_every_ring_kernel_rounds_its_own_f32_result_to_bf16():
     kernel computes in f32: the fast store path and the general one agree bit for bit."""
     rng = np.random.default_rng(77)
     for info in L.kernels():
-        if info["family"] not in ("pipe", "wave") or info["ab_type"] == L.I8:
+        if info["family"] not in ("pipe", "wave") or info["ab_type"] != L.BF16:
             continue
         ta, tb = info["trans_a"], info["trans_b"]
         m, n, k = info["tile_m"] + 40, info["tile_n"] + 24, 136
@@ -186,6 +187,32 @@ def test_random_operands_keep_the_contract_on_every_layout(fmt, trans_a, trans_b
         v = H.f32_from_bf16(got16)
         room = H.bound(k, np.zeros_like(c0), mag) + 2.0**-8 * np.abs(exact) * 1.01
         assert H.outside(v, exact, room) == 0
+
+
+@pytest.mark.parametrize("trans_a,trans_b", LAYOUTS)
+@pytest.mark.parametrize("fmt", [L.F8E4M3, L.F8E5M2])
+def test_fp8_on_the_fp8_matrix_core_keeps_the_contract(fmt, trans_a, trans_b):
+    """The 8-bit floats on v_mfma_f32_32x32x64_f8f6f4 (not widened): every finite pattern of the format at random,
+    subnormals and the largest values included; products exact, the sum within the contract of its exact value."""
+    rng = np.random.default_rng(8 + 4 * fmt + 2 * trans_a + trans_b)
+    m, n, k = 512, 768, 1024
+
+    def patterns(shape):
+        p = rng.integers(0, 256, shape, dtype=np.uint8)
+        bad = ~np.isfinite(H.values(fmt, p))
+        while bad.any():
+            p[bad] = rng.integers(0, 256, int(bad.sum()), dtype=np.uint8)
+            bad = ~np.isfinite(H.values(fmt, p))
+        return p
+
+    a = patterns((k, m) if trans_a else (m, k))
+    b = patterns((n, k) if trans_b else (k, n))
+    A, B = H.values(fmt, a), H.values(fmt, b)
+    exact, mag = H.exact_product(A.T if trans_a else A, B.T if trans_b else B)
+    c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
+    got, ch = run_gemm(fmt, L.F32, m, n, k, a, b, c0, trans_a=trans_a, trans_b=trans_b, accumulate=True)
+    assert ch["name"].startswith("cairn_wave_f8"), ch["name"]
+    assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
 
 
 def test_two_runs_give_the_same_bits():
