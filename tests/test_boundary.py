@@ -146,7 +146,9 @@ def test_the_selector_picks_a_kernel_for_every_baseline_config():
 
 def test_the_selector_falls_back_to_the_generic_kernel_where_chunks_do_not_fit():
     assert choose(L.BF16, L.F32, 65, 63, 33, P, P, P, accumulate=True)["family"] == "generic"  # k % 8
-    assert choose(L.F8E4M3, L.F32, 256, 256, 256, P, P, P, accumulate=True)["family"] == "generic"
+    assert choose(L.F8E4M3, L.F32, 200, 136, 72, P, P, P, accumulate=True)["family"] == "generic"  # rows too short
+    f8 = choose(L.F8E5M2, L.F32, 256, 256, 256, P, P, P, accumulate=True)  # the fp8 matrix core, not widened
+    assert f8["family"] == "wave" and f8["name"] == "cairn_wave_f8e5m2_nn_256x256"
     assert choose(L.BF16, L.F32, 256, 256, 256, P + 2, P, P)["family"] == "generic"  # a off 16 bytes
     assert choose(L.BF16, L.F32, 256, 250, 256, P, P, P)["family"] == "generic"  # n % 4
 
