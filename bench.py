@@ -183,6 +183,50 @@ def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
     return out
 
 
+def operands(ab: int, shape: tuple[int, int], rng) -> np.ndarray:
+    """Random operand patterns of a type: normal values for the 16-bit floats, every finite pattern for the 8-bit
+    floats, uniform bytes for int8."""
+    if ab == L.BF16:
+        return bf16(rng.standard_normal(shape, dtype=np.float32) / np.float32(64.0))
+    if ab == L.F16:
+        return (rng.standard_normal(shape, dtype=np.float32) / np.float32(64.0)).astype(np.float16).view(np.uint16)
+    if ab == L.I8:
+        return rng.integers(-127, 128, shape, dtype=np.int8)
+    pats = rng.integers(0, 256, shape, dtype=np.uint8)
+    nan = (pats & 0x7F) == 0x7F if ab == L.F8E4M3 else (pats & 0x7C) == 0x7C
+    pats[nan] &= 0xBB  # clear an exponent bit: a finite pattern
+    return pats
+
+
+def bench_calibrate(stream, steps: int, warmup: int) -> dict:
+    """Every tiled kernel of the table on a problem its tiles cover whole (4096^3, or 2048^3 for the generic
+    kernel), random operands, its own layout: TFLOP/s (TOPS) and the fraction of its operand type's MFMA peak. The
+    figures the machine card's gemm section records, and the perf model's calibration."""
+    rng = np.random.default_rng(2026)
+    peak = {L.BF16: PEAK_BF16, L.F16: PEAK_BF16, L.I8: PEAK_I8, L.F8E4M3: PEAK_FP8, L.F8E5M2: PEAK_FP8}
+    out = {}
+    for info in L.kernels():
+        fam = info["family"]
+        if fam == "skinny":
+            continue
+        n = 2048 if fam == "generic" else 4096
+        ab = info["ab_type"] if fam != "generic" else L.BF16
+        ta, tb = bool(info["trans_a"]), bool(info["trans_b"])
+        a = hip.Buffer.of(operands(ab, (n, n), rng))
+        b = hip.Buffer.of(operands(ab, (n, n), rng))
+        c = hip.Buffer(n * n * 4)
+        out_type = L.I32 if ab == L.I8 else L.BF16
+        d = L.desc(ab, out_type, n, n, n, a.ptr, b.ptr, c.ptr, trans_a=ta, trans_b=tb, kernel=info["id"])
+        t = timed([d], stream, steps, warmup)
+        rate = 2.0 * n**3 / (t["event_ms_per_step"] * 1e-3) / 1e12
+        out[info["name"]] = {"family": fam, "problem": f"{n}^3", "tflops": round(rate, 1),
+                             "frac": round(rate / peak[ab], 4)}  # fmt: skip
+        log(f"calibrate {info['name']}: {rate:.0f} ({rate / peak[ab]:.1%})")
+        for x in (a, b, c):
+            x.close()
+    return out
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -295,7 +339,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["square", "skinny", "mlp", "all", "traffic"], default="all")
+    ap.add_argument("--only", choices=["square", "skinny", "mlp", "all", "traffic", "calibrate"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--family", choices=["pipe", "wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
@@ -311,6 +355,11 @@ def main() -> int:
     dev = hip.describe(0)
     log("device", dev)
     stream = hip.Stream()
+    if args.only == "calibrate":
+        print(json.dumps({"calibration": bench_calibrate(stream, min(args.steps, 20), min(args.warmup, 3)),
+                          "skinny": bench_skinny(stream, args.steps, args.warmup), "device": dev}), flush=True)  # fmt: skip
+        stream.close()
+        return 0
     if args.only == "traffic":
         print(json.dumps({"traffic_run": bench_traffic(stream, family=args.family)}), flush=True)
         stream.close()
