@@ -6,8 +6,8 @@ bf16 output) with int8 TOPS (W8A8, fused dequant to bf16), as a fraction of the 
 A step is one 4096^3 bf16 GEMM on inputs already resident in HBM. W untimed steps, then exactly K timed steps between
 two synchronizations; `value` is 2 * 4096^3 * K / wall seconds. The same run also measures, as extra records:
 int8 W8A8 4096^3 TOPS; f8e4m3 4096^3 on the fp8 matrix core; the skinny decode GEMMs (m = 1, 4, 16; n = 14336; k = 4096; b stored n x k) in HBM GB/s,
-rotating enough copies of b that the 256 MB MALL cannot hold them; the MLP forward + backward (3 GEMMs); and the
-reference's CPU loop timed on this host (cpu_baseline).
+rotating enough copies of b that the 256 MB MALL cannot hold them; the MLP forward + backward (3 GEMMs); the
+bf16 -> int8 activation quantize in HBM GB/s; and the reference's CPU loop timed on this host (cpu_baseline).
 
 `roofline` is for the dominant kernel (the 4096^3 bf16 GEMM): achieved = 2 * 4096^3 FLOP / its average launch
 duration measured with HIP events on the stream it runs on; peak = 2516.6 TFLOP/s (dense bf16: 256 CUs x 4096
@@ -49,18 +49,18 @@ def bf16(x: np.ndarray) -> np.ndarray:
     return ((u + np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1))) >> 16).astype(np.uint16)
 
 
-def timed(descs: list, stream: hip.Stream, steps: int, warmup: int) -> dict:
+def timed(descs: list, stream: hip.Stream, steps: int, warmup: int, launch=L.run) -> dict:
     """Warm-up, then `steps` launches cycling through `descs` between two synchronizations: wall time per step and
     the events' average kernel time on the stream."""
     for i in range(warmup):
-        L.run(descs[i % len(descs)], stream.handle)
+        launch(descs[i % len(descs)], stream.handle)
     stream.synchronize()
     start, end = hip.Event(), hip.Event()
     hip.synchronize()
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(steps):
-        L.run(descs[i % len(descs)], stream.handle)
+        launch(descs[i % len(descs)], stream.handle)
     end.record(stream)
     end.synchronize()
     hip.synchronize()
@@ -153,6 +153,26 @@ def bench_skinny(stream, steps, warmup) -> dict:
     for b in bs:
         b.close()
     return out
+
+
+def bench_quantize(stream, steps, warmup) -> dict:
+    """The activation quantize before a W8A8 GEMM: bf16 X (8192 x 4096, the MLP layer's input) into int8 with per-row
+    scales computed in the same pass, in HBM GB/s (x read once, q and the scales written once), rotating 4 copies of
+    X (4 x 96 MB) past the 256 MB MALL."""
+    rng = np.random.default_rng(9)
+    m, k, copies = 8192, 4096, 4
+    xs = [hip.Buffer.of(bf16(rng.standard_normal((m, k), dtype=np.float32))) for _ in range(copies)]
+    qs = [hip.Buffer(m * k) for _ in range(copies)]
+    ss = [hip.Buffer(m * 4) for _ in range(copies)]
+    descs = [L.quantize_desc(L.BF16, L.I8, m, k, x.ptr, q.ptr, s.ptr) for x, q, s in zip(xs, qs, ss)]
+    t = timed(descs, stream, max(steps, 4 * copies), warmup, launch=L.quantize)
+    moved = m * k * 2 + m * k + m * 4
+    gbps = moved / (t["event_ms_per_step"] * 1e-3) / 1e9
+    log(f"quantize bf16->int8 {m}x{k}: {gbps:.0f} GB/s")
+    for b in (*xs, *qs, *ss):
+        b.close()
+    return {"metric": "bf16 -> int8 per-row quantize 8192x4096, HBM GB/s", "kernel": "quantize_rows<bf16, i8>",
+            "bytes": moved, "gbps": gbps, "frac": gbps / PEAK_HBM, **t}  # fmt: skip
 
 
 def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
@@ -339,7 +359,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["square", "skinny", "mlp", "all", "traffic", "calibrate"], default="all")
+    ap.add_argument("--only", choices=["square", "skinny", "mlp", "quantize", "all", "traffic", "calibrate"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--family", choices=["pipe", "wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
@@ -389,6 +409,8 @@ def main() -> int:
         record["skinny"] = bench_skinny(stream, args.steps, args.warmup)
     if args.only in ("mlp", "all"):
         record["mlp"] = bench_mlp(stream, args.steps, args.warmup, args.family)
+    if args.only in ("quantize", "all"):
+        record["quantize"] = bench_quantize(stream, args.steps, args.warmup)
     record["device"] = dev
     if not args.no_cpu:
         record["cpu_baseline"] = cpu_baseline()

@@ -17,6 +17,10 @@ F32, F16, BF16, F8E4M3, F8E5M2, I8, I32 = range(7)
 ACT_NONE, ACT_RELU, ACT_GELU = range(3)
 OK, E_SHAPE, E_TYPE, E_KERNEL, E_ARG, E_HIP = range(6)
 DESC_VERSION = 1
+# enum cairn_scale_mode, cairn_quant_status
+SCALE_ROW_ABSMAX, SCALE_ROW, SCALE_TENSOR = range(3)
+QUANT_BAD_SCALE, QUANT_NAN = 1, 2
+QUANTIZE_DESC_VERSION = 1
 FAMILY = {0: "mfma", 1: "generic", 2: "skinny", 3: "pipe", 4: "wave"}
 TYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", F8E4M3: "f8e4m3", F8E5M2: "f8e5m2", I8: "i8", I32: "i32"}
 
@@ -56,6 +60,25 @@ class Desc(C.Structure):
         ("row_scale", C.c_void_p),
         ("col_scale", C.c_void_p),
         ("kernel", C.c_int32),
+    ]
+
+
+class QuantizeDesc(C.Structure):
+    """struct cairn_quantize_desc."""
+
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("x_type", C.c_int32),
+        ("q_type", C.c_int32),
+        ("mode", C.c_int32),
+        ("m", C.c_uint64),
+        ("k", C.c_uint64),
+        ("ldx", C.c_uint64),
+        ("ldq", C.c_uint64),
+        ("x", C.c_void_p),
+        ("q", C.c_void_p),
+        ("scale", C.c_void_p),
+        ("status", C.c_void_p),
     ]
 
 
@@ -103,6 +126,7 @@ SIGNATURES = {
     "cairn_gemm_status_string": (C.c_char_p, [C.c_int]),
     "cairn_gemm_mma": (C.c_int, [C.c_int32, SZ, SZ, SZ, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "cairn_gemm_device_stream": (None, [C.c_void_p]),
+    "cairn_quantize_run": (C.c_int, [C.POINTER(QuantizeDesc), C.c_void_p]),
     **{f"cf_mma_{f}": (None, _MMA) for f in ("f32", "f16", "bf16", "f8e4m3", "f8e5m2")},
     **{f"cf_mma_{f}_device": (None, _MMA) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
     **{f"cq_mma_{f}_device": (None, [C.c_void_p, *_MMA]) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
@@ -142,6 +166,18 @@ def desc(ab_type: int, c_type: int, m: int, n: int, k: int, a=None, b=None, c=No
 
 def run(d: Desc, stream: int | None = None) -> None:
     s = load().cairn_gemm_run(C.byref(d), stream)
+    if s != OK:
+        raise GemmError(s, status_string(s))
+
+
+def quantize_desc(x_type: int, q_type: int, m: int, k: int, x=None, q=None, scale=None, *,
+                  mode: int = SCALE_ROW_ABSMAX, ldx: int = 0, ldq: int = 0, status=None) -> QuantizeDesc:  # fmt: skip
+    """A cairn_quantize_desc; pointers are ints (device addresses) or None."""
+    return QuantizeDesc(QUANTIZE_DESC_VERSION, x_type, q_type, mode, m, k, ldx, ldq, x, q, scale, status)
+
+
+def quantize(d: QuantizeDesc, stream: int | None = None) -> None:
+    s = load().cairn_quantize_run(C.byref(d), stream)
     if s != OK:
         raise GemmError(s, status_string(s))
 

@@ -9,7 +9,6 @@
 // spacing, the dropped bits compared with half a unit.
 #pragma once
 #include <cstdint>
-#include <cstring>
 #include <limits>
 #include <type_traits>
 #include "cairn_runtime.hpp"
@@ -17,16 +16,8 @@
 namespace cr {
 namespace fp {
 
-inline std::uint64_t bits_of(double x) noexcept {
-  std::uint64_t u;
-  std::memcpy(&u, &x, 8);
-  return u;
-}
-inline double double_of(std::uint64_t u) noexcept {
-  double x;
-  std::memcpy(&x, &u, 8);
-  return x;
-}
+CR_HD inline std::uint64_t bits_of(double x) noexcept { return __builtin_bit_cast(std::uint64_t, x); }
+CR_HD inline double double_of(std::uint64_t u) noexcept { return __builtin_bit_cast(double, u); }
 
 template<int E, int M, bool INF> struct Float {
   using Bits = std::conditional_t<(1 + E + M > 8), std::uint16_t, std::uint8_t>;
@@ -60,8 +51,9 @@ template<int E, int M, bool INF> struct Float {
 };
 
 // |x| (finite, not NaN) rounded to T's grid with its exponent unbounded above, ties to even; `over` says the
-// result passes T's largest finite value. Returns the pattern without its sign.
-template<class T> inline typename T::Bits round_magnitude(double x, bool& over) noexcept {
+// result passes T's largest finite value. Returns the pattern without its sign. Host and device: the device
+// quantize kernel takes this path wherever its f32 shortcut cannot decide.
+template<class T> CR_HD inline typename T::Bits round_magnitude(double x, bool& over) noexcept {
   constexpr int M = T::fraction, emin = 1 - T::bias;
   const std::uint64_t u = bits_of(x) & 0x7fffffffffffffffULL;
   over = false;

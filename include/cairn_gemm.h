@@ -171,6 +171,45 @@ void cq_mma_f8e5m2_device(void* stream, size_t m, size_t n, size_t k, size_t cn,
  * what the caller queued there; NULL gives the thread its own stream back (header.py:296-304, cairn_exec.hpp:38-41). */
 void cairn_gemm_device_stream(void* stream);
 
+/*
+ * Device quantize: q[i][j] = quantize[T](x[i][j], scale of row i) for an m x k row-major matrix x, the reference's
+ * element function (src/cairn/runtime/cairn_float.hpp:116-146: x / scale in double, rounded once to nearest even,
+ * saturated at T's finite range) on every element. It makes the operands of the W8A8 and fp8 GEMMs on the device:
+ * activations by rows, and a weight by its output channels when stored n x k (the NT layout). The reference has no
+ * such kernel; its quantize runs an element at a time in user code.
+ *
+ * The scale of each row, per `mode`:
+ *   CAIRN_SCALE_ROW_ABSMAX  computed and written to scale[i]: the largest |x[i][j]| of the row (NaN elements left
+ *                           out) divided by T's largest finite value (127, 448 for E4M3, 57344 for E5M2) in f32,
+ *                           nearest even; 1 for a row of zeros. The row is read once (longer rows than 8192
+ *                           elements: once from HBM, once from cache).
+ *   CAIRN_SCALE_ROW         read from scale[i];
+ *   CAIRN_SCALE_TENSOR      scale[0] for every row.
+ * Where the reference traps, a kernel cannot: a row whose scale is not positive and finite (a given one, or one
+ * computed from a row holding an infinity) is written as zeros and CAIRN_QUANT_BAD_SCALE is ORed into *status; a NaN
+ * quantized to int8 is written as 0 and CAIRN_QUANT_NAN is ORed in. status may be NULL. Queued on `stream` like
+ * cairn_gemm_run: no allocation, no stream or event, no wait.
+ */
+enum cairn_scale_mode { CAIRN_SCALE_ROW_ABSMAX = 0, CAIRN_SCALE_ROW = 1, CAIRN_SCALE_TENSOR = 2 };
+enum cairn_quant_status { CAIRN_QUANT_BAD_SCALE = 1, CAIRN_QUANT_NAN = 2 };
+
+#define CAIRN_QUANTIZE_DESC_VERSION 1u
+
+typedef struct cairn_quantize_desc {
+  uint32_t version; /* CAIRN_QUANTIZE_DESC_VERSION */
+  int32_t x_type;   /* F32, F16 or BF16 */
+  int32_t q_type;   /* I8, F8E4M3 or F8E5M2 */
+  int32_t mode;     /* cairn_scale_mode */
+  uint64_t m, k;
+  uint64_t ldx, ldq; /* elements; 0: packed */
+  const void* x;
+  void* q;
+  float* scale;      /* m floats (ROW_ABSMAX: written; ROW: read), or 1 (TENSOR) */
+  int32_t* status;   /* device word or NULL */
+} cairn_quantize_desc;
+
+int cairn_quantize_run(const cairn_quantize_desc* d, void* stream);
+
 /* The interface identity: defined by the library built with this header (header.py:280-285). */
 extern const char cairn_interface_gemm_gfx950_1[];
 

@@ -19,6 +19,8 @@
  *   oracle_gemm_i8     int8 x int8 -> int32, exact
  *   oracle_dequant     bf16((f32(acc) * sa[i]) * sb[j]), each step an f32 rounding
  *   oracle_gelu        0.5 x (1 + erf(x / sqrt 2)) in fp64 (the erf form; the reference has no GELU)
+ *   oracle_quantize_rows  a matrix quantized row by row with oracle_quantize_* (per-row, per-tensor or computed
+ *                      largest-magnitude scales): the device quantize's contract (the reference has no such kernel)
  *
  * Each function is pinned in tests/test_oracle.py: against golden vectors written from the compiled reference
  * header (tests/golden/), against an exact rational model, and against known answers the reference's docs state.
@@ -291,5 +293,50 @@ void oracle_mma_rows(int f, size_t r0, size_t r1, size_t n, size_t k, float* c, 
 }
 
 /* A decode table the row-parallel variant shares between threads; free with oracle_free. */
+/* oracle_quantize_rows: q[i][j] = quantize[T](x[i][j], s_i) with the reference's element function above. s_i is
+ * scale[i] (mode 1), scale[0] (mode 2), or (mode 0) computed and written to scale[i]: the largest |x[i][j]| of the
+ * row's non-NaN elements divided in f32 by T's largest finite value (127, 448, 57344), or 1 for a row without a
+ * nonzero one. Where the reference would trap the row (a scale not positive and finite) is zeros and bit 1 of
+ * *status is set; a NaN into int8 gives 0 and sets bit 2. x_type is F32, F16 or BF16; q_type 5 (int8), F8E4M3 or
+ * F8E5M2. */
+void oracle_quantize_rows(int x_type, int q_type, int mode, size_t m, size_t k, const void* x, size_t ldx, uint8_t* q,
+                          size_t ldq, float* scale, int* status) {
+  const float range = q_type == 5 ? 127.0f : q_type == F8E4M3 ? 448.0f : 57344.0f;
+  float* row = malloc((k ? k : 1) * sizeof(float));
+  for (size_t i = 0; i < m; ++i) {
+    for (size_t j = 0; j < k; ++j)
+      row[j] = x_type == F32 ? ((const float*)x)[i * ldx + j]
+                             : (float)oracle_decode(x_type, ((const uint16_t*)x)[i * ldx + j]);
+    float s;
+    if (mode == 0) {
+      float top = 0.0f;
+      for (size_t j = 0; j < k; ++j) {
+        const float a = fabsf(row[j]);
+        if (a == a && a > top) top = a;
+      }
+      s = top == 0.0f ? 1.0f : top / range;
+      scale[i] = s;
+    } else {
+      s = scale[mode == 1 ? i : 0];
+    }
+    if (!(s > 0.0f) || !(s <= 3.4028234663852886e38f)) {
+      *status |= 1;
+      memset(q + i * ldq, 0, k);
+      continue;
+    }
+    for (size_t j = 0; j < k; ++j) {
+      int trapped = 0;
+      if (q_type == 5) {
+        const int64_t v = oracle_quantize_int(row[j], s, -128, 127, &trapped);
+        q[i * ldq + j] = (uint8_t)(trapped ? 0 : (int8_t)v);
+      } else {
+        q[i * ldq + j] = (uint8_t)oracle_quantize_float(q_type, row[j], s, &trapped);
+      }
+      if (trapped) *status |= 2;
+    }
+  }
+  free(row);
+}
+
 float* oracle_table(int f) { return f == F32 ? NULL : decode_table(f); }
 void oracle_free(void* p) { free(p); }

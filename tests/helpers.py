@@ -51,6 +51,8 @@ def oracle() -> C.CDLL:
         o.oracle_mma_rows.restype = None
         o.oracle_mma_rows.argtypes = [C.c_int, sz, sz, sz, sz, P, P, P, P]
         o.oracle_table.restype, o.oracle_table.argtypes = P, [C.c_int]
+        o.oracle_quantize_rows.restype = None
+        o.oracle_quantize_rows.argtypes = [C.c_int, C.c_int, C.c_int, sz, sz, P, sz, P, sz, P, C.POINTER(C.c_int)]
         o.oracle_free.restype, o.oracle_free.argtypes = None, [P]
         _oracle = o
     return _oracle
@@ -110,6 +112,20 @@ def narrow_array(fmt: int, x: np.ndarray) -> np.ndarray:
     out = np.zeros(x.shape, dtype=np.uint16)
     oracle().oracle_narrow_f32_array(fmt, x.size, ptr(x), ptr(out))
     return out
+
+
+def quantize_rows(x_type: int, q_type: int, mode: int, x: np.ndarray, k: int, scale: np.ndarray | None = None
+                  ) -> tuple[np.ndarray, np.ndarray, int]:  # fmt: skip
+    """The device quantize's contract on the CPU: x is m rows of ldx = x.shape[1] elements (f32, or 16-bit patterns),
+    of which the first k are quantized. Returns (q m x k uint8 patterns, the scales, the status bits)."""
+    x = np.ascontiguousarray(x)
+    m, ldx = x.shape
+    q = np.zeros((m, max(k, 1)), dtype=np.uint8)
+    s = np.zeros(m, dtype=np.float32) if mode == 0 else np.ascontiguousarray(scale, dtype=np.float32).copy()
+    status = C.c_int(0)
+    oracle().oracle_quantize_rows(x_type, q_type, mode, m, k, ptr(x), ldx, ptr(q), q.shape[1], ptr(s),
+                                  C.byref(status))  # fmt: skip
+    return q[:, :k], s, status.value
 
 
 # ---------------------------------------------------------------- numpy forms used at sizes the C loops cannot reach

@@ -43,8 +43,9 @@ def test_the_library_exports_every_declared_symbol():
 
 
 def test_the_structs_have_the_layout_the_header_states(tmp_path):
-    fields = {"cairn_gemm_desc": [f for f, _ in L.Desc._fields_], "cairn_gemm_kernel": [f for f, _ in L.Kernel._fields_],
-              "cairn_gemm_choice": [f for f, _ in L.Choice._fields_]}  # fmt: skip
+    structs = {"cairn_gemm_desc": L.Desc, "cairn_gemm_kernel": L.Kernel, "cairn_gemm_choice": L.Choice,
+               "cairn_quantize_desc": L.QuantizeDesc}  # fmt: skip
+    fields = {name: [f for f, _ in cls._fields_] for name, cls in structs.items()}
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
     for struct, names in fields.items():
         lines.append(f'printf("{struct} %zu\\n", sizeof({struct}));')
@@ -56,7 +57,7 @@ def test_the_structs_have_the_layout_the_header_states(tmp_path):
     subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
     got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
                                                               check=True).stdout.splitlines())  # fmt: skip
-    for struct, cls in (("cairn_gemm_desc", L.Desc), ("cairn_gemm_kernel", L.Kernel), ("cairn_gemm_choice", L.Choice)):
+    for struct, cls in structs.items():
         assert int(got[struct]) == C.sizeof(cls), struct
         for f in fields[struct]:
             assert int(got[f"{struct}.{f}"]) == getattr(cls, f).offset, (struct, f)
