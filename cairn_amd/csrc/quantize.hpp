@@ -45,22 +45,46 @@ CR_HD inline int exact_i8(float x, float s, bool& trapped) {
 }
 
 // y = x * r within 2^-22 |q| of q and |y| < 256 put q within 2^-14 of y; a y 2^-13 or more from the half-integers
-// about it therefore rounds as q does. |y| >= 256 means |q| > 255: saturated either way. Returns whether y decided.
-CR_HD inline bool try_i8(float y, int& out) {
-  if(__builtin_fabsf(y) >= 256.0f) {
-    out = y < 0.0f ? -128 : 127;
-    return true;
-  }
-  const float n = __builtin_rintf(y);                       // ties to even, as the exact path's
-  const bool ok = __builtin_fabsf(y - n) <= 0.5f - 0x1p-13f;  // the difference is exact; false for a NaN y
-  const int v = int(ok ? n : 0.0f);
-  out = v < -128 ? -128 : (v > 127 ? 127 : v);
-  return ok;
+// about it therefore rounds as q does. |y| >= 256 means |q| > 255: saturated either way, so y is clamped to +-256
+// first (an integer: distance 0). round_i8 gives the candidate and y's distance from it, branch-free (every lane of
+// a wave runs the same instructions); the candidate is q's answer where that distance is at most MARGIN_I8.
+constexpr float MARGIN_I8 = 0.5f - 0x1p-13f;
+CR_HD inline int round_i8(float y, float& dev) {
+  const float c = __builtin_fminf(__builtin_fmaxf(y, -256.0f), 256.0f);
+  const float n = __builtin_rintf(c);  // ties to even, as the exact path's
+  dev = __builtin_fabsf(c - n);        // exact: c and n are within a factor of two, or n is 0
+  return int(__builtin_fminf(__builtin_fmaxf(n, -128.0f), 127.0f));
 }
 
-CR_HD inline int fast_i8(float x, float s, float r, bool& trapped) {
+// Whether y decides: not a NaN (which clamps to a bound and has no int8 answer) and far enough from a tie.
+CR_HD inline bool try_i8(float y, int& out) {
+  float dev;
+  out = round_i8(y, dev);
+  return y == y && dev <= MARGIN_I8;
+}
+
+// Where round_i8 leaves it, y lies within 2^-13 of a half-integer h and q within 2^-12 of it, so q rounds to the
+// integer n nearest y or to its neighbour across h. One fused multiply-add decides which, exactly: x - h * s, rounded
+// once, has the sign of q - h and is zero only at a tie (with scale in the shortcut's range every such difference is
+// a multiple of 2^-149, which the fma represents; an overflow keeps the sign). A tie goes to the even integer. No
+// double arithmetic, and the same answer as the reference's rounding of the double quotient (which is within 2^-37
+// of q, and q is either a tie or at least 2^-25 away from one).
+CR_HD inline int near_i8(float x, float s, float y) {
+  const float c = __builtin_fminf(__builtin_fmaxf(y, -256.0f), 256.0f);
+  const float n = __builtin_rintf(c);
+  const float step = c > n ? 1.0f : -1.0f;
+  const float h = n + 0.5f * step, other = n + step;
+  const float e = __builtin_fmaf(-h, s, x);
+  const bool even = (int(n) & 1) == 0;
+  const float pick = e == 0.0f ? (even ? n : other) : ((e > 0.0f) == (step > 0.0f) ? other : n);
+  return int(__builtin_fminf(__builtin_fmaxf(pick, -128.0f), 127.0f));
+}
+
+// x (not a NaN) into int8 at a scale in the shortcut's range: the shortcut, else the fma decision.
+CR_HD inline int fast_i8(float x, float s, float r) {
   int v;
-  return try_i8(x * r, v) ? v : exact_i8(x, s, trapped);
+  const float y = x * r;
+  return try_i8(y, v) ? v : near_i8(x, s, y);
 }
 
 // An 8-bit float (cr::f8e4m3 or cr::f8e5m2), exactly the reference's steps: the double quotient, its sign (x's, as
@@ -114,9 +138,41 @@ template<class T> CR_HD inline bool try_f8(float x, float y, std::uint32_t& out)
   return dist > TOL;
 }
 
+// Where try_f8 leaves it (y within 8 units of its last place of a midpoint of T's grid), the answer exactly: the
+// midpoint is (2 below + 1) * 2^(spacing - 1), `below` being the grid units under it, and |x| - mid * s by one fused
+// multiply-add has the sign of |q| - mid and is zero only at a tie (with scale in [2^-100, 2^100] the product stays
+// finite and every such difference is a multiple of 2^-149). A tie goes to the even unit; then the encoding of
+// try_f8 (the carry into the next binade, subnormals, saturation).
+template<class T> CR_HD inline std::uint32_t near_f8(float x, float s, float y) {
+  constexpr int M = T::fraction, emin = 1 - T::bias;
+  const std::uint32_t mag = __builtin_bit_cast(std::uint32_t, y) & 0x7fffffffu;
+  const std::uint32_t sign = (__builtin_bit_cast(std::uint32_t, x) >> 31) ? T::sign : 0u;
+  const int e = int(mag >> 23) - 127;
+  const std::uint32_t sig = (mag & 0x7fffffu) | 0x800000u;
+  const int drop = 23 - M + (e < emin ? emin - e : 0);
+  const std::uint32_t below = sig >> drop;
+  const float mid = __builtin_ldexpf(float(2u * below + 1u), e - 23 + drop - 1);
+  const float d = __builtin_fmaf(-mid, s, __builtin_fabsf(x));
+  std::uint32_t n = below + ((d > 0.0f || (d == 0.0f && (below & 1u))) ? 1u : 0u);
+  if(e < emin) return sign | n;
+  int biased = e + T::bias;
+  if(n >> (M + 1)) {
+    n >>= 1;
+    ++biased;
+  }
+  const std::uint32_t frac = n & T::ones;
+  const bool over = biased > int(T::top) || (biased == int(T::top) && (T::infinite || frac == T::ones));
+  return sign | (over ? std::uint32_t(T::largest) : (std::uint32_t(biased) << M) | frac);
+}
+
+// The 8-bit floats' shortcut is sound on a narrower range of scales than int8's: the midpoint times the scale must
+// stay finite in near_f8.
+CR_HD inline bool fast_ok_f8(float s) { return s >= 0x1p-100f && s <= 0x1p100f; }
+
 template<class T> CR_HD inline std::uint32_t fast_f8(float x, float s, float r) {
   std::uint32_t v;
-  return try_f8<T>(x, x * r, v) ? v : exact_f8<T>(x, s);
+  const float y = x * r;
+  return try_f8<T>(x, y, v) ? v : near_f8<T>(x, s, y);
 }
 
 // The divisor the per-row scale is taken against: T's largest finite magnitude.

@@ -200,7 +200,7 @@ typedef struct cairn_quantize_desc {
   int32_t x_type;   /* F32, F16 or BF16 */
   int32_t q_type;   /* I8, F8E4M3 or F8E5M2 */
   int32_t mode;     /* cairn_scale_mode */
-  uint64_t m, k;
+  uint64_t m, k;     /* m < 2^31, k <= 2^28 */
   uint64_t ldx, ldq; /* elements; 0: packed */
   const void* x;
   void* q;

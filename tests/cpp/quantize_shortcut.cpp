@@ -50,8 +50,13 @@ void check_i8(float x, float s) {
     }
   }
   bool trapped = false;
-  const int got = fast_ok(s) ? fast_i8(x, s, r, trapped) : exact_i8(x, s, trapped);
+  const int got = fast_ok(s) && x == x ? fast_i8(x, s, r) : exact_i8(x, s, trapped);
   if(trapped != bool(t) || (!t && got != want)) fail("i8", x, s, trapped ? -999 : got, t ? -999 : want);
+  if(x == x) {  // the exact path alone, at every scale
+    bool dummy = false;
+    const int e = exact_i8(x, s, dummy);
+    if(e != want) fail("i8 exact", x, s, e, want);
+  }
   ++checked;
 }
 
@@ -60,7 +65,7 @@ template<class T> void check_f8(int fmt, float x, float s) {
   int t = 0;
   const long want = long(oracle_quantize_float(fmt, x, s, &t));
   const float r = 1.0f / s;
-  if(fast_ok(s)) {
+  if(fast_ok_f8(s)) {
     std::uint32_t v = 0;
     if(try_f8<T>(x, x * r, v)) {
       ++decided;
@@ -69,8 +74,9 @@ template<class T> void check_f8(int fmt, float x, float s) {
       ++declined;
     }
   }
-  const std::uint32_t got = fast_ok(s) ? fast_f8<T>(x, s, r) : exact_f8<T>(x, s);
+  const std::uint32_t got = fast_ok_f8(s) ? fast_f8<T>(x, s, r) : exact_f8<T>(x, s);
   if(long(got) != want) fail(fmt == 3 ? "e4m3" : "e5m2", x, s, long(got), want);
+  if(long(exact_f8<T>(x, s)) != want) fail("f8 exact", x, s, long(exact_f8<T>(x, s)), want);
   ++checked;
 }
 
@@ -92,7 +98,8 @@ template<class F> void around(double target, float s, int spread, F&& f) {
 int main() {
   std::mt19937_64 rng(20251201);
   std::vector<float> scales = {1.0f, 0.5f, 3.0f, 0.1f, 1.0f / 3.0f, 7.8125e-3f, 1e-3f, 2.5e-2f, 1e-30f, 1e30f,
-                               0x1p-120f, 0x1.fffffep-121f, 0x1p120f, 0x1.000002p120f, 1e-40f, 3e38f, 123.456f};
+                               0x1p-120f, 0x1.fffffep-121f, 0x1p120f, 0x1.000002p120f, 0x1p-100f, 0x1.fffffep-101f,
+                               0x1p100f, 0x1.000002p100f, 0x1.8p-99f, 0x1.8p99f, 1e-40f, 3e38f, 123.456f};
   std::uniform_real_distribution<double> logu(-40.0, 40.0);
   for(int i = 0; i < 48; ++i) scales.push_back(float(std::pow(2.0, logu(rng))) * float(1.0 + (rng() % 1000) / 997.0));
   // Scales as the kernel computes them: a row's largest magnitude over the format's range.

@@ -119,6 +119,7 @@ def test_the_entry_refuses_bad_descriptors_before_any_gpu_call():
     assert status(q_type=L.F16) == L.E_TYPE and status(x_type=L.I8) == L.E_TYPE
     assert status(mode=7) == L.E_ARG and status(scale=None) == L.E_ARG and status(x=None) == L.E_ARG
     assert status(ldx=8) == L.E_SHAPE and status(ldq=3) == L.E_SHAPE and status(m=1 << 31) == L.E_SHAPE
+    assert status(k=(1 << 28) + 8, ldx=0, ldq=0) == L.E_SHAPE
     assert status(m=0) == L.OK  # nothing to do: no launch
     d = L.quantize_desc(L.BF16, L.I8, 4, 16, P, P, P)
     d.version = 9
