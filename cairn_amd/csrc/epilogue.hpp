@@ -8,11 +8,61 @@
 // every combination without changing a bit of what the separate steps give.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include "kernels.hpp"
 #include "mfma.hpp"
 #include "tile.hpp"
 
 namespace cairn::gemm {
+
+// The row scale of each of the lane's rows r0 + 32 i + lane % 32 (1 where there is none or the row is past m).
+template<int FM>
+__device__ __forceinline__ void row_scales(const Params& p, int r0, int lane, float (&rs)[FM]) {
+#pragma unroll
+  for(int i = 0; i < FM; ++i) {
+    const int m = r0 + 32 * i + (lane & 31);
+    rs[i] = p.row_scale && m < p.m ? p.row_scale[m] : 1.0f;
+  }
+}
+
+// The column scales and biases of the lane's 16 columns of a block column starting at n0: quad q, element e is
+// column n0 + 8 q + 4 (lane / 32) + e (1 and -0 where there is none or the column is past n).
+__device__ __forceinline__ void col_terms(const Params& p, int n0, int lane, float (&cs)[4][4], float (&bs)[4][4]) {
+  const bool bias16 = p.bias_type == CAIRN_TYPE_BF16;
+#pragma unroll
+  for(int q = 0; q < 4; ++q) {
+    const int n = n0 + 8 * q + 4 * (lane >> 5);
+    const bool in = n < p.n;  // n and p.n are multiples of 4: the four columns are in or out together
+#pragma unroll
+    for(int e = 0; e < 4; ++e) {
+      cs[q][e] = p.col_scale && in ? p.col_scale[n + e] : 1.0f;
+      if(p.bias && in)
+        bs[q][e] = bias16 ? widen_bf16(static_cast<const std::uint16_t*>(p.bias)[n + e])
+                          : static_cast<const float*>(p.bias)[n + e];
+      else bs[q][e] = -0.0f;
+    }
+  }
+}
+
+// The epilogue's steps on one accumulator value, each an f32 rounding, in the order cairn_gemm.h states. ACT is a
+// template argument: callers branch on p.act once, outside their loops, so that a loop holds only its own
+// activation's code (256 unrolled copies of GELU that a plain store jumps over still crowd the instruction cache).
+template<int ACT>
+__device__ __forceinline__ float apply(float v, float rs, float cs, float bs) {
+  v = v * rs;
+  v = v * cs;
+  v = v + bs;
+  if constexpr(ACT == CAIRN_ACT_RELU) v = v < 0.0f ? 0.0f : v;
+  else if constexpr(ACT == CAIRN_ACT_GELU) v = gelu(v);
+  return v;
+}
+
+// f(integral_constant<ACT>) for the activation p.act names.
+template<class F> __device__ __forceinline__ void with_act(const Params& p, F&& f) {
+  if(p.act == CAIRN_ACT_GELU) f(std::integral_constant<int, CAIRN_ACT_GELU>{});
+  else if(p.act == CAIRN_ACT_RELU) f(std::integral_constant<int, CAIRN_ACT_RELU>{});
+  else f(std::integral_constant<int, CAIRN_ACT_NONE>{});
+}
 
 // RAW: the int32 accumulator itself is the output (int8 operands, c of int32, no epilogue); the kernel is built once
 // each way, so that the two paths do not share (and hoist) the reads of the accumulators.
@@ -39,29 +89,14 @@ __device__ __forceinline__ void finish(const Params& p, const Acc (&acc)[FM][FN]
       return;
     }
   } else {
+  with_act(p, [&](auto act) {
+  constexpr int ACT = decltype(act)::value;
   float rs[FM];
-#pragma unroll
-  for(int i = 0; i < FM; ++i) {
-    const int m = r0 + 32 * i + row;
-    rs[i] = p.row_scale && m < p.m ? p.row_scale[m] : 1.0f;
-  }
-  const bool bias16 = p.bias_type == CAIRN_TYPE_BF16;
+  row_scales<FM>(p, r0, lane, rs);
 #pragma unroll
   for(int j = 0; j < FN; ++j) {
     float cs[4][4], bs[4][4];
-#pragma unroll
-    for(int q = 0; q < 4; ++q) {
-      const int n = c0 + 32 * j + 8 * q + 4 * half;
-      const bool in = n < p.n;  // n and p.n are multiples of 4: the four columns are in or out together
-#pragma unroll
-      for(int e = 0; e < 4; ++e) {
-        cs[q][e] = p.col_scale && in ? p.col_scale[n + e] : 1.0f;
-        if(p.bias && in)
-          bs[q][e] = bias16 ? widen_bf16(static_cast<const std::uint16_t*>(p.bias)[n + e])
-                            : static_cast<const float*>(p.bias)[n + e];
-        else bs[q][e] = -0.0f;
-      }
-    }
+    col_terms(p, c0 + 32 * j, lane, cs, bs);
 #pragma unroll
     for(int i = 0; i < FM; ++i)
 #pragma unroll
@@ -70,19 +105,7 @@ __device__ __forceinline__ void finish(const Params& p, const Acc (&acc)[FM][FN]
         if(!whole && !(m < p.m && n < p.n)) continue;
         float v[4];
 #pragma unroll
-        for(int e = 0; e < 4; ++e) {
-          v[e] = float(acc[i][j][4 * q + e]);
-          v[e] = v[e] * rs[i];
-          v[e] = v[e] * cs[q][e];
-          v[e] = v[e] + bs[q][e];
-        }
-        if(p.act == CAIRN_ACT_RELU) {
-#pragma unroll
-          for(int e = 0; e < 4; ++e) v[e] = v[e] < 0.0f ? 0.0f : v[e];
-        } else if(p.act == CAIRN_ACT_GELU) {
-#pragma unroll
-          for(int e = 0; e < 4; ++e) v[e] = gelu(v[e]);
-        }
+        for(int e = 0; e < 4; ++e) v[e] = apply<ACT>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
         const std::int64_t at = std::int64_t(m) * p.ldc + n;
         if(p.c_type == CAIRN_TYPE_F32) {
           float* out = reinterpret_cast<float*>(c + at * 4);
@@ -107,6 +130,7 @@ __device__ __forceinline__ void finish(const Params& p, const Acc (&acc)[FM][FN]
         }
       }
   }
+  });
   }
 }
 

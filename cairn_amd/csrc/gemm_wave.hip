@@ -56,6 +56,133 @@ __device__ __forceinline__ void fenced_barrier() {
   fence();
 }
 
+// The epilogue of a wave's accumulators, after the main loop (every wave past its last LDS read of the ring): block
+// (i, j) of the wave, quad q of lane l is row m, columns n .. n+3. A bf16 output of a tile wholly inside c goes
+// through LDS so that every store writes whole rows; a plain one (no scales, bias or activation) skips the
+// epilogue's identity steps. Everything else takes finish's quad-by-quad stores.
+// The epilogue terms of a tile, one row scale, column scale and bias a thread (thread t: row row0 + t, column
+// col0 + t), loaded at the kernel's start so that their latency hides behind the main loop; the staged store reads
+// them back from LDS. Identities (1, 1, -0) where a term is absent or out of range.
+struct Terms {
+  float rs = 1.0f, cs = 1.0f, bs = -0.0f;
+};
+
+template<class Sh>
+__device__ __forceinline__ Terms prefetch_terms(const Params& p, int row0, int col0, int t) {
+  static_assert(Sh::BM == 256 && Sh::BN == 256, "a thread a row and a column of the tile");
+  Terms v;
+  const bool staged = p.c_type == CAIRN_TYPE_BF16 && row0 + Sh::BM <= p.m && col0 + Sh::BN <= p.n;
+  if(!staged) return v;  // uniform; the other stores read their terms themselves
+  if(p.row_scale) v.rs = p.row_scale[row0 + t];
+  if(p.col_scale) v.cs = p.col_scale[col0 + t];
+  if(p.bias)
+    v.bs = p.bias_type == CAIRN_TYPE_BF16 ? widen_bf16(static_cast<const std::uint16_t*>(p.bias)[col0 + t])
+                                          : static_cast<const float*>(p.bias)[col0 + t];
+  return v;
+}
+
+template<class Sh, bool RAW, class Acc, int FM, int FN>
+__device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM][FN], char* lds, float* terms,
+                                           const Terms& mine_terms, int wave, int row0, int col0, int wr, int wc,
+                                           int lane) {
+  constexpr int S = Sh::STAGES;
+  const bool plain = !p.row_scale && !p.col_scale && !p.bias && p.act == CAIRN_ACT_NONE;
+  const bool whole = row0 + Sh::BM <= p.m && col0 + Sh::BN <= p.n;
+  if constexpr(!RAW) {
+    if(p.c_type == CAIRN_TYPE_BF16 && whole) {
+      // The wave's WTM x WTN bf16 block goes into its own part of the ring (free once every wave has passed the
+      // barrier), 8 bytes a quad, then comes back 16 bytes a lane, a row of the block per 16 lanes. The 8-byte unit u
+      // of row r sits at unit u ^ (r % 32) of the row, which keeps both the writes (32 rows, one unit each) and the
+      // reads (16 units of one row) on distinct banks; a read of an odd row finds its two halves swapped.
+      static_assert(Sh::WTN * 2 == 256 && Sh::WTM * 256 * Sh::WAVES <= S * Sh::STAGE, "a row of the block is 256 bytes");
+      if(!plain) {
+        const int t = 64 * wave + lane;
+        terms[t] = mine_terms.rs;
+        terms[256 + t] = mine_terms.cs;
+        terms[512 + t] = mine_terms.bs;
+      }
+      fenced_barrier();
+      char* mine = lds + wave * (Sh::WTM * 256);
+      const int h = lane >> 5;
+      auto put = [&](int i, int j, int q, float v0, float v1, float v2, float v3) {
+        const int r = 32 * i + (lane & 31);
+        u32x2 w;
+        w[0] = narrow2_bf16(v0, v1);
+        w[1] = narrow2_bf16(v2, v3);
+        const int unit = (8 * j + 2 * q + h) ^ (r & 31);
+        *reinterpret_cast<u32x2*>(mine + r * 256 + unit * 8) = w;
+      };
+      if(plain) {
+#pragma unroll
+        for(int i = 0; i < FM; ++i)
+#pragma unroll
+          for(int j = 0; j < FN; ++j)
+#pragma unroll
+            for(int q = 0; q < 4; ++q)
+              put(i, j, q, float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]), float(acc[i][j][4 * q + 2]),
+                  float(acc[i][j][4 * q + 3]));
+      } else {
+        with_act(p, [&](auto act) {
+          constexpr int ACT = decltype(act)::value;
+          float rs[FM];
+#pragma unroll
+          for(int i = 0; i < FM; ++i) rs[i] = terms[wr + 32 * i + (lane & 31)];
+#pragma unroll
+          for(int j = 0; j < FN; ++j) {
+            float cs[4][4], bs[4][4];
+#pragma unroll
+            for(int q = 0; q < 4; ++q)
+#pragma unroll
+              for(int e = 0; e < 4; ++e) {
+                const int n = wc + 32 * j + 8 * q + 4 * h + e;
+                cs[q][e] = terms[256 + n];
+                bs[q][e] = terms[512 + n];
+              }
+#pragma unroll
+            for(int i = 0; i < FM; ++i)
+#pragma unroll
+              for(int q = 0; q < 4; ++q) {
+                float v[4];
+#pragma unroll
+                for(int e = 0; e < 4; ++e) v[e] = apply<ACT>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
+                put(i, j, q, v[0], v[1], v[2], v[3]);
+              }
+          }
+        });
+      }
+      const int cl = lane & 15;
+      char* out = static_cast<char*>(p.c) + (std::int64_t(row0 + wr) * p.ldc + col0 + wc) * 2 + 16 * cl;
+#pragma unroll
+      for(int s = 0; s < Sh::WTM / 4; ++s) {
+        const int r = 4 * s + (lane >> 4);
+        u32x4 v = *reinterpret_cast<const u32x4*>(mine + r * 256 + 16 * (cl ^ ((r & 31) >> 1)));
+        if(r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+        *reinterpret_cast<u32x4*>(out + std::int64_t(r) * p.ldc * 2) = v;
+      }
+      return;
+    }
+    if(plain && p.c_type == CAIRN_TYPE_BF16) {  // an edge tile: quad by quad, each checked
+      char* c = static_cast<char*>(p.c);
+#pragma unroll
+      for(int i = 0; i < FM; ++i)
+#pragma unroll
+        for(int j = 0; j < FN; ++j)
+#pragma unroll
+          for(int q = 0; q < 4; ++q) {
+            const int m = row0 + wr + 32 * i + cairn::tile::acc_m(lane);
+            const int n = col0 + wc + 32 * j + cairn::tile::acc_n(lane, q);
+            if(!(m < p.m && n < p.n)) continue;
+            u32x2 w;
+            w[0] = narrow2_bf16(float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]));
+            w[1] = narrow2_bf16(float(acc[i][j][4 * q + 2]), float(acc[i][j][4 * q + 3]));
+            *reinterpret_cast<u32x2*>(c + (std::int64_t(m) * p.ldc + n) * 2) = w;
+          }
+      return;
+    }
+  }
+  finish<RAW>(p, acc, row0 + wr, col0 + wc, lane);
+}
+
 template<class Sh, int OP, bool TA, bool TB, bool RAW>
 __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   static_assert(Sh::WAVES == 4, "one wave a SIMD");
@@ -67,6 +194,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, READS = RA + RB;  // LDS reads a k-step
   static_assert(READS <= 32 && LOADS <= 8, "the interleave below places these between 16 MFMAs");
   __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
+  __shared__ float terms[3 * 256];  // the epilogue's row scales, column scales and biases of the tile
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -75,6 +203,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   int tm, tn;
   cairn::tile::tile_of(int(blockIdx.x), p.tiles_m, p.tiles_n, p.group, tm, tn);
   const int row0 = tm * Sh::BM, col0 = tn * Sh::BN;
+  const Terms mine_terms = RAW ? Terms{} : prefetch_terms<Sh>(p, row0, col0, t);
   const cairn::tile::Panel pa = cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES);
   const cairn::tile::Panel pb = cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES);
   const char* a = static_cast<const char*>(p.a) + pa.start;
@@ -187,65 +316,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   }
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
 
-  // Epilogue: block (i, j) of this wave, quad q of lane l: row m, columns n .. n+3. A plain bf16 output (no scales,
-  // bias or activation) takes the packed conversion, and a tile wholly inside c skips the bounds checks.
-  const bool plain = !p.row_scale && !p.col_scale && !p.bias && p.act == CAIRN_ACT_NONE;
-  if(OP != OP_I8 && plain && p.c_type == CAIRN_TYPE_BF16) {
-    char* c = static_cast<char*>(p.c);
-    const bool whole = row0 + Sh::BM <= p.m && col0 + Sh::BN <= p.n;
-    auto quad = [&](int i, int j, int q, bool check) {
-      const int m = row0 + wr + 32 * i + cairn::tile::acc_m(lane);
-      const int n = col0 + wc + 32 * j + cairn::tile::acc_n(lane, q);
-      if(check && !(m < p.m && n < p.n)) return;
-      u32x2 w;
-      w[0] = narrow2_bf16(float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]));
-      w[1] = narrow2_bf16(float(acc[i][j][4 * q + 2]), float(acc[i][j][4 * q + 3]));
-      *reinterpret_cast<u32x2*>(c + (std::int64_t(m) * p.ldc + n) * 2) = w;
-    };
-    if(whole) {
-      // Through LDS, so that every store writes whole rows: the wave's WTM x WTN bf16 block goes into its own part
-      // of the ring (free once every wave has passed the barrier), 8 bytes a quad, then comes back 16 bytes a lane,
-      // a row of the block per 16 lanes. The 8-byte unit u of row r sits at unit u ^ (r % 32) of the row, which keeps
-      // both the writes (32 rows, one unit each) and the reads (16 units of one row) on distinct banks; a read of an
-      // odd row finds its two halves swapped.
-      static_assert(Sh::WTN * 2 == 256 && Sh::WTM * 256 * Sh::WAVES <= S * Sh::STAGE, "a row of the block is 256 bytes");
-      fenced_barrier();
-      char* mine = lds + wave * (Sh::WTM * 256);
-      const int h = lane >> 5;
-#pragma unroll
-      for(int i = 0; i < FM; ++i) {
-        const int r = 32 * i + (lane & 31);
-#pragma unroll
-        for(int j = 0; j < FN; ++j)
-#pragma unroll
-          for(int q = 0; q < 4; ++q) {
-            u32x2 w;
-            w[0] = narrow2_bf16(float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]));
-            w[1] = narrow2_bf16(float(acc[i][j][4 * q + 2]), float(acc[i][j][4 * q + 3]));
-            const int unit = (8 * j + 2 * q + h) ^ (r & 31);
-            *reinterpret_cast<u32x2*>(mine + r * 256 + unit * 8) = w;
-          }
-      }
-      const int cl = lane & 15;
-      char* out = c + (std::int64_t(row0 + wr) * p.ldc + col0 + wc) * 2 + 16 * cl;
-#pragma unroll
-      for(int s = 0; s < Sh::WTM / 4; ++s) {
-        const int r = 4 * s + (lane >> 4);
-        u32x4 v = *reinterpret_cast<const u32x4*>(mine + r * 256 + 16 * (cl ^ ((r & 31) >> 1)));
-        if(r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
-        *reinterpret_cast<u32x4*>(out + std::int64_t(r) * p.ldc * 2) = v;
-      }
-    } else {
-#pragma unroll
-      for(int i = 0; i < FM; ++i)
-#pragma unroll
-        for(int j = 0; j < FN; ++j)
-#pragma unroll
-          for(int q = 0; q < 4; ++q) quad(i, j, q, true);
-    }
-    return;
-  }
-  finish<RAW>(p, acc, row0 + wr, col0 + wc, lane);
+  store_tile<Sh, RAW>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
 }
 
 // The 8-bit floats on the same ring: one v_mfma_f32_32x32x64_f8f6f4 covers a whole stage (64 bytes of k), so a
@@ -266,6 +337,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, STEP_READS = RA + RB, READS = 2 * STEP_READS;
   static_assert(READS <= 32 && Sh::LOADS_A <= 4 && Sh::LOADS_B <= 4, "the interleave below");
   __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
+  __shared__ float terms[3 * 256];  // the epilogue's row scales, column scales and biases of the tile
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -274,6 +346,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   int tm, tn;
   cairn::tile::tile_of(int(blockIdx.x), p.tiles_m, p.tiles_n, p.group, tm, tn);
   const int row0 = tm * Sh::BM, col0 = tn * Sh::BN;
+  const Terms mine_terms = false ? Terms{} : prefetch_terms<Sh>(p, row0, col0, t);
   const cairn::tile::Panel pa = cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES);
   const cairn::tile::Panel pb = cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES);
   const char* a = static_cast<const char*>(p.a) + pa.start;
@@ -370,7 +443,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   }
   if(it < T) iteration(it, std::integral_constant<int, 0>{});
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
-  finish<false>(p, acc, row0 + wr, col0 + wc, lane);
+  store_tile<Sh, false>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
 }
 
 template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave8(const Params& p, hipStream_t s) {

@@ -133,6 +133,45 @@ def test_every_ring_kernel_rounds_its_own_f32_result_to_bf16():
         assert np.array_equal(b16, H.bf16_from_f32(f32)), info["name"]
 
 
+@pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_RELU])
+def test_every_ring_kernel_applies_the_epilogue_in_its_stated_order(act):
+    """Row and column scales, a bias and an activation on every LDS-ring kernel of every operand type, bf16 out:
+    whole tiles take the LDS-staged store, edge tiles the checked one, and both equal the stated steps applied in f32
+    to what the same kernel computes without them: bf16(act((f32(acc) * rs[i]) * cs[j] + bias[j]))."""
+    rng = np.random.default_rng(78 + act)
+    ran = 0
+    for info in L.kernels():
+        if info["family"] not in ("pipe", "wave"):
+            continue
+        ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
+        m, n, k = info["tile_m"] + 40, info["tile_n"] + 24, 144
+        if not fits(info, m, n, k):
+            continue
+        if t == L.I8:
+            a = rng.integers(-127, 128, (k, m) if ta else (m, k), dtype=np.int8)
+            b = rng.integers(-127, 128, (n, k) if tb else (k, n), dtype=np.int8)
+        elif t in (L.F8E4M3, L.F8E5M2):
+            a = H.encode(t, rng.standard_normal(m * k).clip(-8, 8)).reshape((k, m) if ta else (m, k))
+            b = H.encode(t, rng.standard_normal(k * n).clip(-8, 8)).reshape((n, k) if tb else (k, n))
+        else:
+            a = H.normal_bf16(rng, (k, m) if ta else (m, k), 1.0)
+            b = H.normal_bf16(rng, (n, k) if tb else (k, n), 1.0)
+        rs = rng.uniform(0.25, 2.0, m).astype(np.float32)
+        cs = rng.uniform(0.25, 2.0, n).astype(np.float32)
+        bias = H.normal_bf16(rng, (n,), 4.0)
+        raw, _ = run_gemm(t, L.I32 if t == L.I8 else L.F32, m, n, k, a, b, trans_a=ta, trans_b=tb, kernel=info["id"])
+        got, _ = run_gemm(t, L.BF16, m, n, k, a, b, trans_a=ta, trans_b=tb, row_scale=rs, col_scale=cs, bias=bias,
+                          bias_type=L.BF16, act=act, kernel=info["id"])  # fmt: skip
+        v = raw.astype(np.float32) * rs[:, None]
+        v = v * cs[None, :]
+        v = v + H.f32_from_bf16(bias)[None, :]
+        if act == L.ACT_RELU:
+            v = np.where(v < 0, np.float32(0), v)
+        assert np.array_equal(got, H.bf16_from_f32(v)), info["name"]
+        ran += 1
+    assert ran >= 10
+
+
 @pytest.mark.parametrize("name", ["cairn_pipe_bf16_nn_256x256", "cairn_wave_bf16_nn_256x256"])
 def test_bf16_outputs_round_ties_to_even_keep_subnormals_and_overflow(name):
     """Outputs exact in f32 that sit on bf16 rounding ties: near 1 (c = b0 +- 2^-8), among the subnormals
