@@ -16,7 +16,16 @@
 
 namespace cr {
 
-[[noreturn]] inline void trap() noexcept { std::abort(); }
+// A broken guard stops the program: the host aborts; a device lane raises the wave's trap, which ends the kernel
+// with an error the next wait on its stream reports (src/cairn/runtime/cairn_runtime.hpp:59-70 does the same with
+// CUDA's trap).
+[[noreturn]] CR_HD inline void trap() noexcept {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_trap();
+#else
+  std::abort();
+#endif
+}
 
 // a * b, or a trap where it overflows.
 template<class T> inline T mul(T a, T b) noexcept {
