@@ -15,7 +15,10 @@
 // tiling runs a 1 x n x k call as 64 x 64 tiles (src/cairn/runtime/cairn_tensor.hpp:206-221).
 #include <hip/hip_runtime.h>
 #include <type_traits>
+#include <utility>
 #include "kernels.hpp"
+#include "mfma.hpp"
+#include "ring.hpp"
 
 namespace cairn::gemm {
 
@@ -131,6 +134,107 @@ __global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
   }
 }
 
+// The streaming form, for n wide enough to give most CUs a workgroup of 64 columns (n >= 8192): b's 64 rows and a's
+// 16 rows go from HBM straight into an LDS ring by `buffer_load ... lds`, KC bytes of k a row a stage, S stages, so
+// that up to S - 1 stages (3 x 40 KiB a CU) are in flight without a register held for them, each load 2 rows x 512
+// contiguous bytes. Wave w multiplies rows 16 w .. 16 w + 15 of b (the workgroup's columns) over the whole stage, so
+// its accumulator is whole at the end and nothing is reduced across waves. One barrier a stage, as the GEMM ring
+// (gemm_wave.hip): past it the stage has landed for every wave and the stage before it is free for the refill.
+// A row's 16-byte units are stored swizzled, unit u of row r at u ^ (r % 32), so the 16 rows an MFMA operand read
+// takes are on distinct banks; the swizzle is applied by choosing which global unit each lane fetches.
+// f(integral_constant<U>) for U = 0 .. N-1.
+template<int N, class F> __device__ __forceinline__ void unrolled_loads(F&& f) {
+  [&]<int... U>(std::integer_sequence<int, U...>) {
+    (f(std::integral_constant<int, U>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
+}
+
+template<int S, int KC>
+__global__ void __launch_bounds__(256) skinny_ring(Params p) {
+  constexpr int ROWS_B = 64, ROWS_A = 16, UNITS = KC / 16, ROWS_PER_LOAD = 1024 / KC;
+  constexpr int B_BYTES = ROWS_B * KC, STAGE = (ROWS_B + ROWS_A) * KC;
+  constexpr int LOADS_B = ROWS_B / ROWS_PER_LOAD / 4, LOADS_A = ROWS_A / ROWS_PER_LOAD / 4;  // a wave's, a stage
+  constexpr int LOADS = LOADS_B + LOADS_A;
+  static_assert((KC == 256 || KC == 512 || KC == 1024) && LOADS_B % 4 == 0 && LOADS_A <= 4, "loads go out in groups of four");
+  __shared__ __attribute__((aligned(1024))) char lds[S * STAGE];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int n0 = int(blockIdx.x) * ROWS_B;
+  const int rows = p.n - n0 < ROWS_B ? p.n - n0 : ROWS_B;  // b's rows of this workgroup
+  const unsigned ring = lds_address(lds);
+
+  // b's rows n0 .., a's rows 0 .., each through its own range (zero fill past the last valid byte).
+  Dma dma;
+  const Dma::Rsrc rb = Dma::resource(static_cast<const char*>(p.b) + std::int64_t(n0) * p.ldb * 2,
+                                     std::int64_t(rows - 1) * p.ldb * 2 + std::int64_t(p.k) * 2);
+  const Dma::Rsrc ra = Dma::resource(static_cast<const char*>(p.a), std::int64_t(p.m - 1) * p.lda * 2 + std::int64_t(p.k) * 2);
+  const int kbytes = p.k * 2, T = (kbytes + KC - 1) / KC;
+  // Load j of this wave's stage (j < LOADS_B: b's rows 2 (8 w + j) + lane / 32; else a's 2 (2 w + j - LOADS_B) + ..),
+  // this lane's unit: the global unit that lands at LDS position lane % 32 of its row.
+  auto offset = [&](int j, int st) {
+    const bool is_b = j < LOADS_B;
+    const int q = is_b ? LOADS_B * wave + j : LOADS_A * wave + j - LOADS_B;  // the load's 1 KiB block of the stage
+    const int r = ROWS_PER_LOAD * q + lane / UNITS, pos = lane % UNITS;
+    const int u = pos ^ (r & (UNITS - 1));
+    const int kb = st * KC + 16 * u;
+    const bool in = kb < kbytes && (is_b ? r < rows : r < p.m);
+    return in ? int(r * (is_b ? p.ldb : p.lda) * 2 + kb) : 0x7fffffff;
+  };
+  auto issue = [&](int st) {  // this wave's loads of stage st into buffer st % S, M0 once for each four
+    const unsigned base = ring + unsigned((st % S) * STAGE);
+#pragma unroll
+    for(int g = 0; g < LOADS_B / 4; ++g) {
+      dma.set_base(base + unsigned(LOADS_B * wave + 4 * g) * 1024u);
+      dma.template load_lds_imm<0>(rb, offset(4 * g, st));
+      dma.template load_lds_imm<1>(rb, offset(4 * g + 1, st));
+      dma.template load_lds_imm<2>(rb, offset(4 * g + 2, st));
+      dma.template load_lds_imm<3>(rb, offset(4 * g + 3, st));
+    }
+    dma.set_base(base + unsigned(B_BYTES) + unsigned(LOADS_A * wave) * 1024u);
+    unrolled_loads<LOADS_A>([&](auto u) { dma.template load_lds_imm<decltype(u)::value>(ra, offset(LOADS_B + decltype(u)::value, st)); });
+  };
+
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  f32x4 acc = f32x4{0, 0, 0, 0};
+  const int row = lane & 15, piece = lane >> 4;
+  const int rb_row = 16 * wave + row;  // this lane's b row (the MFMA's column) and a row
+  for(int st = 0; st < S - 1; ++st) issue(st);
+  for(int st = 0; st < T; ++st) {
+    wait_loads<(S - 2) * LOADS>();                   // stage st has landed (this wave's part)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of stage st - 1 are done
+    barrier();                                         // every wave's: stage st is whole, stage st - 1 is free
+    issue(st + S - 1);                                 // into stage st - 1's buffer; past k it reads nothing
+    const char* stage = lds + (st % S) * STAGE;
+#pragma unroll
+    for(int s = 0; s < KC / 64; ++s) {  // the stage's k-steps of 32 elements
+      const int u = 4 * s + piece;
+      const w32x4 xb = *reinterpret_cast<const w32x4*>(stage + rb_row * KC + 16 * (u ^ (rb_row & (UNITS - 1))));
+      const w32x4 xa = *reinterpret_cast<const w32x4*>(stage + B_BYTES + row * KC + 16 * (u ^ row));
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa), __builtin_bit_cast(bf16x8, xb), acc,
+                                                    0, 0, 0);
+    }
+  }
+  wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
+
+  // Lane l holds rows 4 (l / 16) .. +3 (of a) of column n0 + 16 w + l % 16.
+  const int n = n0 + rb_row;
+  if(n >= p.n) return;
+#pragma unroll
+  for(int r = 0; r < 4; ++r) {
+    const int m = 4 * piece + r;
+    if(m >= p.m) continue;
+    float v[1] = {acc[r]};
+    epilogue<1>(p, m, n, v);
+    const std::int64_t at = std::int64_t(m) * p.ldc + n;
+    if(p.c_type == CAIRN_TYPE_F32) {
+      float* out = static_cast<float*>(p.c) + at;
+      *out = p.accumulate ? *out + v[0] : v[0];
+    } else {
+      static_cast<std::uint16_t*>(p.c)[at] = p.c_type == CAIRN_TYPE_BF16 ? narrow_bf16(v[0]) : narrow_f16(v[0]);
+    }
+  }
+}
+
 }  // namespace cairn::gemm
 
 // The width of a workgroup's columns for n: n spread evenly over the 256 CUs, in multiples of 8, from 8 up to the
@@ -142,6 +246,12 @@ int cairn_skinny_width(int n) {
 }
 
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
+  // At least 128 workgroups of 64 columns: the streaming form, 4 stages of 512 bytes (measured against 8 of 256
+  // bytes, 4.6 TB/s, and 2 of 1 KiB, 4.4 TB/s: depth in flight and 512-byte runs both count).
+  if(p.n >= 8192) {
+    hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 512>), dim3(unsigned((p.n + 63) / 64)), dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
   constexpr int GROUPS = 4, WAVES = 4, CH = 8;  // measured best of 2 / 4 / 8 waves and chunks of 8 / 16 steps
   const int width = cairn_skinny_width(p.n);
   const dim3 grid(unsigned((p.n + width - 1) / width));

@@ -95,13 +95,14 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
       // of row r sits at unit u ^ (r % 32) of the row, which keeps both the writes (32 rows, one unit each) and the
       // reads (16 units of one row) on distinct banks; a read of an odd row finds its two halves swapped.
       static_assert(Sh::WTN * 2 == 256 && Sh::WTM * 256 * Sh::WAVES <= S * Sh::STAGE, "a row of the block is 256 bytes");
-      if(!plain) {
+      fenced_barrier();  // every wave is past its last read of the ring
+      if(!plain) {       // uniform
         const int t = 64 * wave + lane;
         terms[t] = mine_terms.rs;
         terms[256 + t] = mine_terms.cs;
         terms[512 + t] = mine_terms.bs;
+        fenced_barrier();
       }
-      fenced_barrier();
       char* mine = lds + wave * (Sh::WTM * 256);
       const int h = lane >> 5;
       auto put = [&](int i, int j, int q, float v0, float v1, float v2, float v3) {
@@ -186,6 +187,7 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
 template<class Sh, int OP, bool TA, bool TB, bool RAW>
 __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   static_assert(Sh::WAVES == 4, "one wave a SIMD");
+  constexpr int TERMS_AT = Sh::WTM * 256 * Sh::WAVES;  // the first byte of the ring the staged store leaves free
   using M = Mfma<OP>;
   using Acc = typename M::Acc;
   constexpr bool AK = !TA, BKM = TB;
@@ -194,7 +196,14 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, READS = RA + RB;  // LDS reads a k-step
   static_assert(READS <= 32 && LOADS <= 8, "the interleave below places these between 16 MFMAs");
   __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
-  __shared__ float terms[3 * 256];  // the epilogue's row scales, column scales and biases of the tile
+  // The epilogue's row scales, column scales and biases of the tile (3 KiB): past the staged store's part of the
+  // ring where the ring has room (a 5-stage ring), else their own array.
+  float* terms;
+  if constexpr(S * Sh::STAGE >= TERMS_AT + 3 * 1024) terms = reinterpret_cast<float*>(lds + TERMS_AT);
+  else {
+    __shared__ float own[3 * 256];
+    terms = own;
+  }
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -329,6 +338,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
 template<class Sh, int OP, bool TA, bool TB>
 __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   static_assert(Sh::WAVES == 4 && Sh::ES == 1, "one wave a SIMD, 8-bit operands");
+  constexpr int TERMS_AT = Sh::WTM * 256 * Sh::WAVES;  // the first byte of the ring the staged store leaves free
   using M = Mfma<OP>;
   using Acc = typename M::Acc;
   constexpr bool AK = !TA, BKM = TB;
@@ -337,7 +347,14 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, STEP_READS = RA + RB, READS = 2 * STEP_READS;
   static_assert(READS <= 32 && Sh::LOADS_A <= 4 && Sh::LOADS_B <= 4, "the interleave below");
   __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
-  __shared__ float terms[3 * 256];  // the epilogue's row scales, column scales and biases of the tile
+  // The epilogue's row scales, column scales and biases of the tile (3 KiB): past the staged store's part of the
+  // ring where the ring has room (a 5-stage ring), else their own array.
+  float* terms;
+  if constexpr(S * Sh::STAGE >= TERMS_AT + 3 * 1024) terms = reinterpret_cast<float*>(lds + TERMS_AT);
+  else {
+    __shared__ float own[3 * 256];
+    terms = own;
+  }
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);

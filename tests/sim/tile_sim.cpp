@@ -495,6 +495,7 @@ int main() {
   pipe_shapes<cairn::pipe::Shape<128, 128, 1, 4>>();
   pipe_shapes<cairn::pipe::Shape<256, 256, 2, 4, 4>>();
   pipe_shapes<cairn::pipe::Shape<256, 256, 1, 4, 4>>();
+  pipe_shapes<cairn::pipe::Shape<256, 256, 2, 5, 4>>();  // a 5-stage ring (the index math is the same)
   pipe_shapes<cairn::pipe::Shape<256, 128, 2, 4, 4>>();
   pipe_shapes<cairn::pipe::Shape<128, 128, 2, 4, 4>>();
   pipe_shapes<cairn::pipe::Shape<128, 128, 1, 4, 4>>();
