@@ -134,7 +134,7 @@ __global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
   }
 }
 
-// The streaming form, for n wide enough to give most CUs a workgroup of 64 columns (n >= 8192): b's 64 rows and a's
+// The streaming form, for n >= 8192 (workgroups of 64 columns, at least 128 of them): b's 64 rows and a's
 // 16 rows go from HBM straight into an LDS ring by `buffer_load ... lds`, KC bytes of k a row a stage, S stages, so
 // that up to S - 1 stages (3 x 40 KiB a CU) are in flight without a register held for them, each load 2 rows x 512
 // contiguous bytes. Wave w multiplies rows 16 w .. 16 w + 15 of b (the workgroup's columns) over the whole stage, so
@@ -150,7 +150,7 @@ template<int N, class F> __device__ __forceinline__ void unrolled_loads(F&& f) {
 }
 
 template<int S, int KC>
-__global__ void __launch_bounds__(256) skinny_ring(Params p) {
+__global__ void __launch_bounds__(256) skinny_ring(Params p, int width) {
   constexpr int ROWS_B = 64, ROWS_A = 16, UNITS = KC / 16, ROWS_PER_LOAD = 1024 / KC;
   constexpr int B_BYTES = ROWS_B * KC, STAGE = (ROWS_B + ROWS_A) * KC;
   constexpr int LOADS_B = ROWS_B / ROWS_PER_LOAD / 4, LOADS_A = ROWS_A / ROWS_PER_LOAD / 4;  // a wave's, a stage
@@ -159,8 +159,8 @@ __global__ void __launch_bounds__(256) skinny_ring(Params p) {
   __shared__ __attribute__((aligned(1024))) char lds[S * STAGE];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int n0 = int(blockIdx.x) * ROWS_B;
-  const int rows = p.n - n0 < ROWS_B ? p.n - n0 : ROWS_B;  // b's rows of this workgroup
+  const int n0 = int(blockIdx.x) * width;                // width <= 64: the columns of this workgroup
+  const int rows = p.n - n0 < width ? p.n - n0 : width;  // b's rows of this workgroup
   const unsigned ring = lds_address(lds);
 
   // b's rows n0 .., a's rows 0 .., each through its own range (zero fill past the last valid byte).
@@ -217,8 +217,8 @@ __global__ void __launch_bounds__(256) skinny_ring(Params p) {
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
 
   // Lane l holds rows 4 (l / 16) .. +3 (of a) of column n0 + 16 w + l % 16.
+  if(rb_row >= rows) return;  // a column past this workgroup's (the next one's, or past n)
   const int n = n0 + rb_row;
-  if(n >= p.n) return;
 #pragma unroll
   for(int r = 0; r < 4; ++r) {
     const int m = 4 * piece + r;
@@ -248,8 +248,12 @@ int cairn_skinny_width(int n) {
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // At least 128 workgroups of 64 columns: the streaming form, 4 stages of 512 bytes (measured against 8 of 256
   // bytes, 4.6 TB/s, and 2 of 1 KiB, 4.4 TB/s: depth in flight and 512-byte runs both count).
+  // 64 columns a workgroup (16 a wave): spreading n = 14336 over all 256 CUs, 56 columns each, measured slower
+  // (4.8 against 5.0 TB/s) than 224 workgroups of 64.
   if(p.n >= 8192) {
-    hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 512>), dim3(unsigned((p.n + 63) / 64)), dim3(256), 0, s, p);
+    const int width = 64;
+    hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 512>), dim3(unsigned((p.n + width - 1) / width)), dim3(256), 0, s,
+                       p, width);
     return hipGetLastError();
   }
   constexpr int GROUPS = 4, WAVES = 4, CH = 8;  // measured best of 2 / 4 / 8 waves and chunks of 8 / 16 steps
