@@ -134,7 +134,7 @@ __global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
   }
 }
 
-// The streaming form, for n >= 8192 (workgroups of 64 columns, at least 128 of them): b's 64 rows and a's
+// The ring form, for m > 4 and n >= 8192 (workgroups of 64 columns, at least 128 of them): b's 64 rows and a's
 // 16 rows go from HBM straight into an LDS ring by `buffer_load ... lds`, KC bytes of k a row a stage, S stages, so
 // that up to S - 1 stages (3 x 40 KiB a CU) are in flight without a register held for them, each load 2 rows x 512
 // contiguous bytes. Wave w multiplies rows 16 w .. 16 w + 15 of b (the workgroup's columns) over the whole stage, so
@@ -235,6 +235,99 @@ __global__ void __launch_bounds__(256) skinny_ring(Params p, int width) {
   }
 }
 
+// The row-streaming form, for m = 1 and k <= 4096 (a decode step's one token): a wave owns a contiguous
+// run of b's rows (the output's columns) and reads each row front to back, 1 KiB a load (64 lanes x 16 bytes), so
+// every wave streams one contiguous region of HBM, as a plain copy does. The arithmetic is small enough for the
+// vector ALUs: lane l holds a's 16-byte pieces at the same k as its pieces of b (loaded once), multiplies and adds
+// in f32 (every product of two bf16 exact, each sum one rounding: the contract), and the wave's 64 partial sums of a
+// row meet in a fixed DPP pattern, so two runs give the same bits. The next row's loads are issued before the
+// current row is summed: two rows of a wave in flight, KCH KiB each.
+template<int M, int KCH>
+__global__ void __launch_bounds__(256) skinny_rows(Params p, int per_wave) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = int(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(t >> 6);
+  const int first = wave * per_wave;
+  const int last = first + per_wave < p.n ? first + per_wave : p.n;  // rows [first, last) of b
+  if(first >= last) return;
+  const int kbytes = p.k * 2;
+  // Piece c of a row: bytes 1024 c + 16 l; past k it reads zeros.
+  auto at = [&](int c) { return 1024 * c + 16 * lane < kbytes ? 1024 * c + 16 * lane : 0x7fffffff; };
+  const __amdgpu_buffer_rsrc_t ra = span(p.a, (std::int64_t(M - 1) * p.lda + p.k) * 2);
+  w32x4 xa[M][KCH];
+#pragma unroll
+  for(int i = 0; i < M; ++i)
+#pragma unroll
+    for(int c = 0; c < KCH; ++c) {
+      const int o = at(c);
+      xa[i][c] = i < p.m ? __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               ra, o == 0x7fffffff ? o : int(i * p.lda * 2) + o, 0, 0))
+                         : w32x4{0u, 0u, 0u, 0u};
+    }
+  const char* brow = static_cast<const char*>(p.b) + std::int64_t(first) * p.ldb * 2;
+  const __amdgpu_buffer_rsrc_t rb = span(brow, (std::int64_t(last - first - 1) * p.ldb + p.k) * 2);
+  w32x4 xb[2][KCH];
+  auto load = [&](int r, w32x4 (&dst)[KCH]) {  // row first + r
+#pragma unroll
+    for(int c = 0; c < KCH; ++c) {
+      const int o = at(c);
+      dst[c] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, o == 0x7fffffff ? o : int(r * p.ldb * 2) + o, 0, 0));
+    }
+  };
+  auto wave_sum = [&](float v) {  // the same fixed pattern for every row: quads, half rows, rows, then the 4 rows
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float s2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float s3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (s0 + s1) + (s2 + s3);
+  };
+  auto row = [&](int r, const w32x4 (&xr)[KCH]) {
+    float acc[M];
+#pragma unroll
+    for(int i = 0; i < M; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for(int c = 0; c < KCH; ++c)
+#pragma unroll
+      for(int e = 0; e < 4; ++e) {
+        const std::uint32_t wb = xr[c][e];
+        const float b0 = __builtin_bit_cast(float, wb << 16), b1 = __builtin_bit_cast(float, wb & 0xffff0000u);
+#pragma unroll
+        for(int i = 0; i < M; ++i) {
+          const std::uint32_t wa = xa[i][c][e];
+          acc[i] = __builtin_fmaf(__builtin_bit_cast(float, wa << 16), b0, acc[i]);
+          acc[i] = __builtin_fmaf(__builtin_bit_cast(float, wa & 0xffff0000u), b1, acc[i]);
+        }
+      }
+    const int n = first + r;
+#pragma unroll
+    for(int i = 0; i < M; ++i) {
+      float v[1] = {wave_sum(acc[i])};
+      if(i >= p.m || lane != 0) continue;
+      epilogue<1>(p, i, n, v);
+      const std::int64_t o = std::int64_t(i) * p.ldc + n;
+      if(p.c_type == CAIRN_TYPE_F32) {
+        float* out = static_cast<float*>(p.c) + o;
+        *out = p.accumulate ? *out + v[0] : v[0];
+      } else {
+        static_cast<std::uint16_t*>(p.c)[o] = p.c_type == CAIRN_TYPE_BF16 ? narrow_bf16(v[0]) : narrow_f16(v[0]);
+      }
+    }
+  };
+  const int rows = last - first;
+  load(0, xb[0]);
+  int r = 0;
+  for(; r + 2 <= rows; r += 2) {  // two rows an iteration, so that each buffer is named at compile time
+    load(r + 1, xb[1]);
+    row(r, xb[0]);
+    if(r + 2 < rows) load(r + 2, xb[0]);
+    row(r + 1, xb[1]);
+  }
+  if(r < rows) row(r, xb[0]);
+}
+
 }  // namespace cairn::gemm
 
 // The width of a workgroup's columns for n: n spread evenly over the 256 CUs, in multiples of 8, from 8 up to the
@@ -246,11 +339,17 @@ int cairn_skinny_width(int n) {
 }
 
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
-  // At least 128 workgroups of 64 columns: the streaming form, 4 stages of 512 bytes (measured against 8 of 256
-  // bytes, 4.6 TB/s, and 2 of 1 KiB, 4.4 TB/s: depth in flight and 512-byte runs both count).
-  // 64 columns a workgroup (16 a wave): spreading n = 14336 over all 256 CUs, 56 columns each, measured slower
-  // (4.8 against 5.0 TB/s) than 224 workgroups of 64.
-  if(p.n >= 8192) {
+  // Three forms, chosen by what measured fastest on the decode shape (n = 14336, k = 4096) in one run of all three:
+  // m = 1, whole rows a wave (5.2 TB/s, against 5.1 for the register form and 4.6 for the ring); m = 5 .. 16 and
+  // n >= 8192, the LDS ring (4.6 against 4.4 TB/s at m = 16); otherwise the register form (m = 2: 4.9 TB/s, where
+  // whole rows are bound by their arithmetic, 4.3; m = 4: 4.6 against 4.5).
+  constexpr int ROW_WAVES = 2048;  // 8 a CU
+  const int per_wave = (p.n + ROW_WAVES - 1) / ROW_WAVES;
+  if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(per_wave) * p.ldb * 2 < 0x7f000000LL) {
+    hipLaunchKernelGGL((cairn::gemm::skinny_rows<1, 8>), dim3(unsigned(ROW_WAVES / 4)), dim3(256), 0, s, p, per_wave);
+    return hipGetLastError();
+  }
+  if(p.m > 4 && p.n >= 8192) {  // 64 columns a workgroup (16 a wave); 56 a workgroup over all 256 CUs was slower
     const int width = 64;
     hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 512>), dim3(unsigned((p.n + width - 1) / width)), dim3(256), 0, s,
                        p, width);

@@ -345,9 +345,11 @@ def test_skinny_decode_shapes_keep_the_contract(m):
     assert H.outside(v, exact, room) == 0
 
 
-# n >= 8192 takes the streaming form (64 columns a workgroup, 512-byte stages of k): column and k tails there too.
+# m > 4 with n >= 8192 takes the ring form (64 columns a workgroup, 512-byte stages of k), m = 1 with n >= 2048 and
+# k <= 4096 the row-streaming one (whole rows of b a wave), the rest the register form: tails in each.
 @pytest.mark.parametrize("m,n,k", [(1, 8, 8), (3, 100, 72), (16, 33, 4104), (7, 14336, 24), (5, 200, 4160),
-                                   (2, 72, 1000), (3, 8200, 4104), (16, 9000, 520), (1, 8192, 8), (9, 8257, 1032)])
+                                   (2, 72, 1000), (3, 8200, 4104), (16, 9000, 520), (1, 8192, 8), (9, 8257, 1032),
+                                   (1, 4100, 4096), (1, 3000, 1000), (1, 20000, 264), (1, 2048, 4088), (5, 8256, 4096)])
 def test_skinny_tails_keep_the_contract(m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = H.normal_bf16(rng, (m, k), 1.0)
