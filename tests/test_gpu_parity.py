@@ -19,6 +19,7 @@ import sys
 
 import numpy as np
 import pytest
+from scipy.special import erf
 
 import helpers as H
 from cairn_amd import hip
@@ -387,3 +388,41 @@ def test_int8_4096_cubed_is_bit_exact():
     got, _ = run_gemm(L.I8, L.I32, n, n, n, a, b)
     want = a.astype(np.float64) @ b.astype(np.float64)
     assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_the_mlp_layer_at_full_size_keeps_the_contract():
+    """C3 at BASELINE.json's size, on the GPU in full: the forward Y = GELU(X W + b) (NN, bias and GELU fused, bf16
+    out), dX = dY W^T (NT) and dW = X^T dY (TN), with X 8192 x 4096, W 4096 x 11008, dY 8192 x 11008. Checked
+    against the exact fp64 product on a sample of 256 output rows of each (the host's BLAS): each output within
+    the contract's bound plus its bf16 rounding, GELU's slope (<= 1.13) carried through."""
+    rng = np.random.default_rng(3)
+    m, k, n = 8192, 4096, 11008
+    x = H.normal_bf16(rng, (m, k), 1.0)
+    w = H.normal_bf16(rng, (k, n), 0.02)
+    bias = H.normal_bf16(rng, (n,), 0.02)
+    dy = H.normal_bf16(rng, (m, n), 1.0)
+    xv, wv, dyv = H.values(L.BF16, x), H.values(L.BF16, w), H.values(L.BF16, dy)
+    rows = np.sort(rng.choice(m, 256, replace=False))
+    o = H.oracle()
+
+    y, ch = run_gemm(L.BF16, L.BF16, m, n, k, x, w, bias=bias, bias_type=L.BF16, act=L.ACT_GELU)
+    say("mlp forward ran on", ch["name"])
+    exact, mag = H.exact_product(xv[rows], wv)
+    pre = exact + H.values(L.BF16, bias)[None, :]
+    want = 0.5 * pre * (1.0 + erf(pre / np.sqrt(2.0)))  # the oracle's GELU (oracle_gelu), vectorized
+    assert abs(float(want[0, 0]) - o.oracle_gelu(float(pre[0, 0]))) <= 1e-15 * max(1.0, abs(float(want[0, 0])))
+    room = 1.2 * H.bound(k, np.zeros(1), mag + np.abs(pre)) + 2.0**-8 * np.abs(want) * 1.01 + 1e-6
+    assert H.outside(H.f32_from_bf16(y[rows]), want, room) == 0
+
+    dx, ch = run_gemm(L.BF16, L.BF16, m, k, n, dy, w, trans_b=True)
+    say("mlp dX ran on", ch["name"])
+    exact, mag = H.exact_product(dyv[rows], wv.T)
+    room = H.bound(n, np.zeros(1), mag) + 2.0**-8 * np.abs(exact) * 1.01
+    assert H.outside(H.f32_from_bf16(dx[rows]), exact, room) == 0
+
+    dw, ch = run_gemm(L.BF16, L.BF16, k, n, m, x, dy, trans_a=True)
+    say("mlp dW ran on", ch["name"])
+    wrows = np.sort(rng.choice(k, 256, replace=False))
+    exact, mag = H.exact_product(xv[:, wrows].T, dyv)
+    room = H.bound(m, np.zeros(1), mag) + 2.0**-8 * np.abs(exact) * 1.01
+    assert H.outside(H.f32_from_bf16(dw[wrows]), exact, room) == 0
