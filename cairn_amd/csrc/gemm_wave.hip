@@ -50,6 +50,10 @@ template<int N, class F> __device__ __forceinline__ void unrolled(F&& f) {
 // No instruction is scheduled across this point.
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// The walk's registers as if rewritten here: the compiler cannot compute a later stage's resource from an earlier one
+// ahead of time (which gathers the scalar work of an unrolled loop into one gap between MFMAs).
+__device__ __forceinline__ void pin(Walk& w) { asm volatile("" : "+s"(w.at), "+s"(w.left)); }
+
 __device__ __forceinline__ void fenced_barrier() {
   fence();
   asm volatile("s_barrier" ::: "memory");
@@ -232,23 +236,30 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
 #pragma unroll
     for(int j = 0; j < FN; ++j) acc[i][j] = Acc{};
   u32x4 xa[2][FM], xb[2][FN];
+  // The lane's transpose-read offset of each 32-column block of an M/N-major operand at k-step 0, half 0; the
+  // other k-step and half add mnmajor_step, an immediate.
+  int ta_off[FM], tb_off[FN];
+#pragma unroll
+  for(int i = 0; i < FM; ++i) ta_off[i] = AK ? 0 : mnmajor_fragment<ES, Sh::BM>(wr + 32 * i, 0, 0, lane);
+#pragma unroll
+  for(int j = 0; j < FN; ++j) tb_off[j] = BKM ? 0 : mnmajor_fragment<ES, Sh::BN>(wc + 32 * j, 0, 0, lane);
 
   // Read X of a k-step's READS: a's fragments first (one b128 each, or two transpose halves), then b's.
-  auto read = [&](auto buf, const char* stage, int s, auto x) {
-    constexpr int X = decltype(x)::value, BUF = decltype(buf)::value;
+  auto read = [&](auto buf, const char* stage, auto s, auto x) {
+    constexpr int X = decltype(x)::value, BUF = decltype(buf)::value, KS = decltype(s)::value;
     if constexpr(X < RA) {
-      if constexpr(AK) xa[BUF][X] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(wr + 32 * X, s, lane));
+      if constexpr(AK) xa[BUF][X] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(wr + 32 * X, KS, lane));
       else {
-        const u32x2 h = transpose_half<ES>(stage + mnmajor_fragment<ES, Sh::BM>(wr + 32 * (X / 2), s, X % 2, lane));
+        const u32x2 h = transpose_half<ES>(stage + ta_off[X / 2] + mnmajor_step<ES, Sh::BM>(KS, X % 2));
         xa[BUF][X / 2][2 * (X % 2)] = h[0];
         xa[BUF][X / 2][2 * (X % 2) + 1] = h[1];
       }
     } else {
       constexpr int Y = X - RA;
       const char* bs = stage + Sh::A_BYTES;
-      if constexpr(BKM) xb[BUF][Y] = *reinterpret_cast<const u32x4*>(bs + kmajor_fragment(wc + 32 * Y, s, lane));
+      if constexpr(BKM) xb[BUF][Y] = *reinterpret_cast<const u32x4*>(bs + kmajor_fragment(wc + 32 * Y, KS, lane));
       else {
-        const u32x2 h = transpose_half<ES>(bs + mnmajor_fragment<ES, Sh::BN>(wc + 32 * (Y / 2), s, Y % 2, lane));
+        const u32x2 h = transpose_half<ES>(bs + tb_off[Y / 2] + mnmajor_step<ES, Sh::BN>(KS, Y % 2));
         xb[BUF][Y / 2][2 * (Y % 2)] = h[0];
         xb[BUF][Y / 2][2 * (Y % 2) + 1] = h[1];
       }
@@ -258,26 +269,35 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
     constexpr int X = decltype(x)::value, BUF = decltype(buf)::value, I = X / FN, J = X % FN;
     acc[I][J] = M::step(xb[BUF][J], xa[BUF][I], acc[I][J]);
   };
-  auto stage_of = [&](int st) { return lds + (st % S) * Sh::STAGE; };
+  // A stage's place in the ring: `slot` is its index there, a constant in the unrolled steady loop (so that every LDS
+  // address and M0 value is an immediate) or an int.
+  auto stage_at = [&](auto slot) { return lds + int(slot) * Sh::STAGE; };
   using LA = Loader<Sh, Sh::BM, AK, Dma>;
   using LB = Loader<Sh, Sh::BN, BKM, Dma>;
-  auto at_of = [&](int st) { return ring + unsigned((st % S) * Sh::STAGE); };
-  // One operand's part of a stage: M0 once, then its loads by immediate offset.
-  auto load_a = [&](const auto& r, int st, auto u) {
-    if constexpr(decltype(u)::value == 0) dma.set_base(LA::base(at_of(st), wave));
-    la.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  // One operand's part of stage st (ring slot `slot`): M0 once, then its loads by immediate offset; with `tail`, each
+  // chunk checked against k (Loader::load_imm), else as set up (Loader::load_steady, for stages that end at or before
+  // k and those past the last).
+  using Tail = std::true_type;
+  using Steady = std::false_type;
+  auto load_a = [&](const auto& r, int st, auto slot, auto u, auto tail) {
+    constexpr int U = decltype(u)::value;
+    if constexpr(U == 0) dma.set_base(LA::base(ring + unsigned(int(slot) * Sh::STAGE), wave));
+    if constexpr(decltype(tail)::value) la.template load_imm<U>(dma, r, st, p.k);
+    else la.template load_steady<U>(dma, r);
   };
-  auto load_b = [&](const auto& r, int st, auto u) {
-    if constexpr(decltype(u)::value == 0) dma.set_base(LB::base(at_of(st) + Sh::A_BYTES, wave));
-    lb.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  auto load_b = [&](const auto& r, int st, auto slot, auto u, auto tail) {
+    constexpr int U = decltype(u)::value;
+    if constexpr(U == 0) dma.set_base(LB::base(ring + unsigned(int(slot) * Sh::STAGE + Sh::A_BYTES), wave));
+    if constexpr(decltype(tail)::value) lb.template load_imm<U>(dma, r, st, p.k);
+    else lb.template load_steady<U>(dma, r);
   };
   auto stage_a = [&](int st) {
     const auto r = la.resource(dma, a, pa.bytes, p.lda, st);
-    unrolled<Sh::LOADS_A>([&](auto u) { load_a(r, st, u); });
+    unrolled<Sh::LOADS_A>([&](auto u) { load_a(r, st, st % S, u, Tail{}); });
   };
   auto stage_b = [&](int st) {
     const auto r = lb.resource(dma, b, pb.bytes, p.ldb, st);
-    unrolled<Sh::LOADS_B>([&](auto u) { load_b(r, st, u); });
+    unrolled<Sh::LOADS_B>([&](auto u) { load_b(r, st, st % S, u, Tail{}); });
   };
 
   using B0 = std::integral_constant<int, 0>;
@@ -288,28 +308,56 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
     stage_b(st);
   }
   stage_a(S - 1);
+  using K0 = std::integral_constant<int, 0>;
+  using K1 = std::integral_constant<int, 1>;
   wait_loads<(S - 2) * LOADS + Sh::LOADS_A>();
   fenced_barrier();
-  unrolled<READS>([&](auto x) { read(B0{}, stage_of(0), 0, x); });
+  unrolled<READS>([&](auto x) { read(B0{}, stage_at(K0{}), K0{}, x); });
+
+  // The loop's buffer resources, walked a stage at a time: b's from stage S - 1 (iteration 0 loads its b), a's from
+  // stage S. Each is computed after MFMAs 8 (its bytes) and 9 (the resource) of the k-step before the one that loads
+  // it, and its walk advanced after MFMA 12: slots with no other issue.
+  Walk wa = walk<Sh, AK>(a, pa.bytes, p.lda, S), wb = walk<Sh, BKM>(b, pb.bytes, p.ldb, S - 1);
+  Dma::Rsrc rb = Dma::resource(wb), ra;
+  unsigned records;
+  wb.advance();
+  // Iterations before `steady` load only stages that end at or before k, or (where k is a whole number of stages)
+  // stages past the last: their loads skip the per-chunk k check. The others load the last, partial, stage.
+  const int steady = p.k % Sh::BK == 0 ? T : (T - 1 - S > 0 ? T - 1 - S : 0);
 
   // Placing: reads 2 X and 2 X + 1 of a k-step after MFMA X, so that they complete well before their MFMAs; load u of
   // a half stage after MFMA 4 u + 2.
   static_assert(Sh::LOADS_A <= 4 && Sh::LOADS_B <= 4, "a half stage's loads take every fourth MFMA");
-  for(int it = 0; it < T; ++it) {
-    const char* cur = stage_of(it);
-    const char* nxt = stage_of(it + 1);
+  static_assert(READS <= 16, "MFMAs 8, 9 and 12 of a k-step issue no read");
+  // Iteration `it`, its stage in ring slot `slot` (= it % S; the next in slot + 1, b's loads this iteration go to
+  // slot + S - 1 and a's to slot itself, all mod S).
+  auto iteration = [&](int it, auto slot, auto tail) {
+    const auto next = [&] {
+      if constexpr(std::is_integral_v<decltype(slot)>) return (slot + 1) % S;
+      else return std::integral_constant<int, (decltype(slot)::value + 1) % S>{};
+    }();
+    const auto slot_b = [&] {
+      if constexpr(std::is_integral_v<decltype(slot)>) return (slot + S - 1) % S;
+      else return std::integral_constant<int, (decltype(slot)::value + S - 1) % S>{};
+    }();
+    const char* cur = stage_at(slot);
+    const char* nxt = stage_at(next);
     const int sb = it + S - 1, sa = it + S;  // the stages whose b's, then a's, loads this iteration issues
-    const auto rb = lb.resource(dma, b, pb.bytes, p.ldb, sb);
     unrolled<16>([&](auto x) {
       constexpr int X = decltype(x)::value;
       mfma(B0{}, x);
       fence();
-      if constexpr(2 * X < READS) read(B1{}, cur, 1, std::integral_constant<int, 2 * X>{});
-      if constexpr(2 * X + 1 < READS) read(B1{}, cur, 1, std::integral_constant<int, 2 * X + 1>{});
-      if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_B) load_b(rb, sb, std::integral_constant<int, X / 4>{});
+      if constexpr(2 * X < READS) read(B1{}, cur, K1{}, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(B1{}, cur, K1{}, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_B) load_b(rb, sb, slot_b, std::integral_constant<int, X / 4>{}, tail);
+      if constexpr(X == 8) records = wa.records();
+      if constexpr(X == 9) ra = Dma::resource(wa.at, records);
+      if constexpr(X == 12) {
+        wa.advance();
+        pin(wa);
+      }
       fence();
     });
-    const auto ra = la.resource(dma, a, pa.bytes, p.lda, sa);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wait_loads<(S - 2) * LOADS>();
     fenced_barrier();
@@ -317,12 +365,23 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
       constexpr int X = decltype(x)::value;
       mfma(B1{}, x);
       fence();
-      if constexpr(2 * X < READS) read(B0{}, nxt, 0, std::integral_constant<int, 2 * X>{});
-      if constexpr(2 * X + 1 < READS) read(B0{}, nxt, 0, std::integral_constant<int, 2 * X + 1>{});
-      if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_A) load_a(ra, sa, std::integral_constant<int, X / 4>{});
+      if constexpr(2 * X < READS) read(B0{}, nxt, K0{}, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(B0{}, nxt, K0{}, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_A) load_a(ra, sa, slot, std::integral_constant<int, X / 4>{}, tail);
+      if constexpr(X == 8) records = wb.records();
+      if constexpr(X == 9) rb = Dma::resource(wb.at, records);
+      if constexpr(X == 12) {
+        wb.advance();
+        pin(wb);
+      }
       fence();
     });
-  }
+  };
+  // The steady iterations S at a time, each of the S with its ring slot known; then the rest one at a time.
+  int it = 0;
+  for(; it + S <= steady; it += S)
+    unrolled<S>([&](auto u) { iteration(it + decltype(u)::value, u, Steady{}); });
+  for(; it < T; ++it) iteration(it, it % S, Tail{});
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
 
   store_tile<Sh, RAW>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);

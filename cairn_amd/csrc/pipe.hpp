@@ -150,6 +150,12 @@ template<class Sh, int R, bool KMAJOR, class Mem> struct Loader {
     const int o = tail && k0 + kidx[U] >= k ? cairn::tile::OUTSIDE : offset[U];
     mem.template load_lds_imm<U>(r, o);
   }
+  // load_imm for a stage that ends at or before k: no chunk of it reaches past k, so the lane's offset stands as set
+  // up. The main loop also issues it for stages past the last, which no MFMA reads: their bytes are never used, and
+  // the walked resource (Walk) keeps every load inside the panel.
+  template<int U, class Rsrc> CAIRN_HD void load_steady(Mem& mem, const Rsrc& r) const {
+    mem.template load_lds_imm<U>(r, offset[U]);
+  }
   template<class Dst> CAIRN_HD static Dst base(Dst dst, int w) { return dst + LOADS * w * 1024; }
   // Whether every lane's offset of load u stays at or above 1024 u for leading dimension ld: the smallest offset of
   // load u is (wave 0, lane 0) slot 64 u, row 16 u of a K-major operand (64-byte rows a stage), k row
@@ -163,6 +169,34 @@ template<class Sh, int R, bool KMAJOR, class Mem> struct Loader {
     for(int u = 0; u < LOADS; ++u) load_one(mem, r, dst, st, k, u, w);
   }
 };
+
+// An operand's buffer resource walked one stage at a time, as the main loop moves through k: the stage's first byte
+// and the panel's bytes from there, moved by one stage's step with additions only. records() clamps the bytes to
+// [0, 2^31 - 1] exactly as Mem::resource does, from the 32-bit halves (the scalar unit has no signed 64-bit compare,
+// and one on the vector unit costs an issue slot between MFMAs). walk(st) equals Loader::resource(st).
+struct Walk {
+  const char* at;
+  std::int64_t left, step;
+  CAIRN_HD unsigned records() const {
+    const std::uint32_t hi = std::uint32_t(std::uint64_t(left) >> 32), lo = std::uint32_t(left);
+    return std::int32_t(hi) < 0 ? 0u : (hi != 0u || lo > 0x7fffffffu ? 0x7fffffffu : lo);
+  }
+  CAIRN_HD void advance() {
+    at += step;
+    left -= step;
+  }
+};
+template<class Sh, bool KMAJOR> CAIRN_HD Walk walk(const char* panel, std::int64_t bytes, std::int64_t ld, int st) {
+  const std::int64_t step = KMAJOR ? std::int64_t(Sh::ROW) : std::int64_t(Sh::BK) * ld * Sh::ES;
+  return Walk{panel + st * step, bytes - st * step, step};
+}
+
+// mnmajor_fragment(n0, s, h, l) - mnmajor_fragment(n0, 0, 0, l): the same for every lane and n0, because k-step s
+// and half h move the k row by a multiple of the swizzle's period (4 rows of 16-bit elements, 8 of bytes). So a
+// lane's transpose reads of one column block share one address register and differ by this immediate.
+template<int ES, int R> constexpr int mnmajor_step(int s, int h) {
+  return (ES == 2 ? 16 * s + 4 * h : 32 * s + 8 * h) * R * ES;
+}
 
 // The transpose reads as the hardware performs them, for the simulator: 16-lane groups, lane q of a group supplies
 // 8 bytes; for 16-bit elements row r of the 4 x 16 block is lanes 4r .. 4r+3 (4 elements each) and lane q receives

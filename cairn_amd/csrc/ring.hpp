@@ -33,6 +33,11 @@ struct Dma {
     const std::uint64_t addr = reinterpret_cast<std::uintptr_t>(base);
     return Rsrc{unsigned(addr), unsigned(addr >> 32) & 0xffffu, unsigned(capped), 0x00020000u};
   }
+  __device__ static Rsrc resource(const char* at, unsigned records) {
+    const std::uint64_t addr = reinterpret_cast<std::uintptr_t>(at);
+    return Rsrc{unsigned(addr), unsigned(addr >> 32) & 0xffffu, records, 0x00020000u};
+  }
+  __device__ static Rsrc resource(const Walk& w) { return resource(w.at, w.records()); }
   __device__ static void load_lds(Rsrc r, unsigned lds_at, int offset) {
     const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_at);
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(offset), "s"(r)

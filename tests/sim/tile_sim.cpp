@@ -57,6 +57,7 @@ struct HostMem {
   Rsrc resource(const char* base, std::int64_t bytes) {
     return Rsrc{base, bytes < 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffffLL : bytes)};
   }
+  Rsrc resource(const cairn::pipe::Walk& w) { return Rsrc{w.at, std::int64_t(w.records())}; }
   template<int N> void read(Rsrc r, int off, std::uint32_t* out) {
     std::memset(out, 0, N);
     if(off < 0) bad = true;
@@ -260,6 +261,7 @@ template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k,
 
 bool bad_read = false;
 bool conflict = false;
+bool stepped_off = false;
 // gfx950 LDS: 64 banks of 4 bytes. A ds_read_b128 is served 16 lanes a clock, a 64-bit read 32 lanes a clock; a
 // phase without conflicts touches each bank once.
 void check_banks(const int addr[64], int bytes) {
@@ -282,6 +284,7 @@ struct HostDma {
   int lane = 0;
   using Rsrc = HostMem::Rsrc;
   Rsrc resource(const char* base, std::int64_t bytes) { return mem->resource(base, bytes); }
+  Rsrc resource(const cairn::pipe::Walk& w) { return mem->resource(w); }
   void load_lds(Rsrc r, char* wave_base, int offset) {
     const u32x4 v = mem->load16(r, offset);
     lds->write16(int(reinterpret_cast<std::uint8_t*>(wave_base) - ring) + 16 * lane, v);
@@ -299,6 +302,24 @@ struct HostDma {
 template<class L, class D, class R, std::size_t... U>
 void imm_loads(const L& l, D& d, const R& r, int st, int k, std::index_sequence<U...>) {
   (l.template load_imm<int(U)>(d, r, st, k), ...);
+}
+// The main loop's loads of a stage that ends at or before k (or lies past the last): no per-chunk k check.
+template<class L, class D, class R, std::size_t... U>
+void steady_loads(const L& l, D& d, const R& r, std::index_sequence<U...>) {
+  (l.template load_steady<int(U)>(d, r), ...);
+}
+// The walked resource of stage st (the main loop's) must be the one Loader::resource computes.
+template<class Sh, bool KMAJOR>
+HostMem::Rsrc walked(HostMem& mem, const char* panel, std::int64_t bytes, std::int64_t ld, int st) {
+  cairn::pipe::Walk w = cairn::pipe::walk<Sh, KMAJOR>(panel, bytes, ld, st > 2 ? st - 2 : 0);
+  for(int i = st > 2 ? st - 2 : 0; i < st; ++i) w.advance();
+  const HostMem::Rsrc got = mem.resource(w), want = mem.resource(panel + (KMAJOR ? std::int64_t(st) * Sh::ROW : std::int64_t(st) * Sh::BK * ld * Sh::ES),
+                                                                 bytes - (KMAJOR ? std::int64_t(st) * Sh::ROW : std::int64_t(st) * Sh::BK * ld * Sh::ES));
+  if(got.base != want.base || got.bytes != want.bytes) {
+    std::printf("walk: stage %d resource differs from Loader::resource\n", st);
+    ++failures;
+  }
+  return got;
 }
 
 template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad, int group) {
@@ -338,6 +359,8 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
     }
     std::vector<double> acc(static_cast<std::size_t>(BM * BN), 0.0);
     const int T = (k + Sh::BK - 1) / Sh::BK;
+    using LAx = cairn::pipe::Loader<Sh, BM, AK, HostDma>;
+    using LBx = cairn::pipe::Loader<Sh, BN, BKM, HostDma>;
     for(int st = 0; st < T; ++st) {
       HostLds lds(Sh::STAGE);  // one stage of the ring (the ring's other stages are the same code at other bases)
       HostDma da{&mem_a, &lds, lds.bytes.data()}, db{&mem_b, &lds, lds.bytes.data()};
@@ -349,7 +372,12 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
       char* stage_b = stage_a + Sh::A_BYTES;
       for(int gt = 0; gt < 256; ++gt) {
         da.lane = db.lane = gt & 63;
-        if(imm) {
+        if(imm && (st + 1) * Sh::BK <= k) {  // the main loop's steady loads, through the walked resources
+          da.set_base(LA::base(stage_a, gt >> 6));
+          steady_loads(la[gt], da, walked<Sh, AK>(mem_a, a, pa.bytes, lda, st), std::make_index_sequence<LA::LOADS>{});
+          db.set_base(LB::base(stage_b, gt >> 6));
+          steady_loads(lb[gt], db, walked<Sh, BKM>(mem_b, b, pb.bytes, ldb, st), std::make_index_sequence<LB::LOADS>{});
+        } else if(imm) {
           da.set_base(LA::base(stage_a, gt >> 6));
           imm_loads(la[gt], da, la[gt].resource(da, a, pa.bytes, lda, st), st, k, std::make_index_sequence<LA::LOADS>{});
           db.set_base(LB::base(stage_b, gt >> 6));
@@ -387,6 +415,10 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
                     for(int l = 0; l < 64; ++l) {
                       addr[l] = base + (R == BM ? frag_mn<ES, BM>(row0_, s, h, l) : frag_mn<ES, BN>(row0_, s, h, l));
                       if(addr[l] < base || addr[l] + 8 > base + R * 64) bad_read = true;
+                      // The kernel's form: the lane's k-step 0, half 0 offset, then an immediate step.
+                      const int stepped = R == BM ? frag_mn<ES, BM>(row0_, 0, 0, l) + cairn::pipe::mnmajor_step<ES, BM>(s, h)
+                                                  : frag_mn<ES, BN>(row0_, 0, 0, l) + cairn::pipe::mnmajor_step<ES, BN>(s, h);
+                      if(base + stepped != addr[l]) stepped_off = true;
                     }
                     check_banks(addr, 8);
                     std::uint8_t got[64][8];
@@ -398,6 +430,7 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
               gather(AK, 0, BM, wr + 32 * i, fa);
               gather(BKM, Sh::A_BYTES, BN, wc + 32 * j, fb);
               if(bad_read) FAIL("pipe %s: a fragment read off its operand's stage", lay);
+              if(stepped_off) FAIL("pipe %s %dx%d es=%d: a transpose read's k-step and half are not an immediate step", lay, BM, BN, ES);
               if(conflict) FAIL("pipe %s %dx%d es=%d: a fragment read phase has an LDS bank conflict", lay, BM, BN, ES);
               double P[32][32], Q[32][32];
               constexpr int CE = 16 / ES;
@@ -421,6 +454,23 @@ template<class Sh, bool TA, bool TB> void run_pipe(int m, int n, int k, int pad,
                 }
             }
       }
+    }
+    // Where k is a whole number of stages, the one-wave-a-SIMD kernel's main loop also issues steady loads for the S
+    // stages past the last (into ring buffers no MFMA reads again): each must stay inside its matrix or read zeros.
+    if(Sh::WAVES == 4 && k % Sh::BK == 0 && LAx::imm_fits(lda) && LBx::imm_fits(ldb)) {
+      HostLds spare(Sh::STAGE);
+      HostDma da{&mem_a, &spare, spare.bytes.data()}, db{&mem_b, &spare, spare.bytes.data()};
+      char* stage_a = reinterpret_cast<char*>(spare.bytes.data());
+      for(int st = T; st < T + Sh::STAGES; ++st)
+        for(int gt = 0; gt < 256; ++gt) {
+          da.lane = db.lane = gt & 63;
+          da.set_base(LAx::base(stage_a, gt >> 6));
+          steady_loads(la[gt], da, walked<Sh, AK>(mem_a, a, pa.bytes, lda, st), std::make_index_sequence<LAx::LOADS>{});
+          db.set_base(LBx::base(stage_a + Sh::A_BYTES, gt >> 6));
+          steady_loads(lb[gt], db, walked<Sh, BKM>(mem_b, b, pb.bytes, ldb, st), std::make_index_sequence<LBx::LOADS>{});
+        }
+      if(mem_a.bad || mem_b.bad) FAIL("pipe %s %dx%d es=%d %dx%dx%d: a load past the last stage outside its matrix", lay, BM, BN, ES, m, n, k);
+      if(da.negative || db.negative) FAIL("pipe %s: an offset register below zero past the last stage", lay);
     }
     for(int wave = 0; wave < Sh::WAVES; ++wave) {
       int wr, wc;
@@ -458,7 +508,8 @@ template<class Sh> void pipe_shapes() {
                          {Sh::BM, Sh::BN, 64 / Sh::ES, 0, 4},
                          {Sh::BM + MN, Sh::BN + 2 * MN, 3 * CE, 16, 1},
                          {2 * Sh::BM + 4 * MN, Sh::BN - MN, 200 / CE * CE, 16, 2},
-                         {264 / MN * MN, Sh::BN + MN, 37 * CE, 0, 4}};
+                         {264 / MN * MN, Sh::BN + MN, 37 * CE, 0, 4},
+                         {Sh::BM + MN, Sh::BN, 8 * (64 / Sh::ES), 8, 3}};
   for(auto& s : list) {
     run_pipe<Sh, false, false>(s[0], s[1], s[2], s[3], s[4]);
     run_pipe<Sh, false, true>(s[0], s[1], s[2], s[3], s[4]);

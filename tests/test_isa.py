@@ -67,7 +67,46 @@ def test_the_main_loop_writes_m0_twice_per_stage(assembly):
         assert loops, name
         loop = max(loops, key=lambda seg: sum(x.startswith("v_mfma") for x in seg))  # the main loop
         fp8 = "wave8_gemm" in name  # one 32x32x64 MFMA a block and stage; the int8 layout's two k-steps otherwise
-        assert sum("m0" in x for x in loop) == (4 if fp8 else 2), name  # the fp8 loop is unrolled by two stages
-        assert sum(x.startswith("v_mfma") for x in loop) == 32, name
-        assert sum(x == "s_barrier" for x in loop) == (2 if fp8 else 1), name
+        mfmas = sum(x.startswith("v_mfma") for x in loop)
+        stages = mfmas // (16 if fp8 else 32)
+        # The fp8 loop is unrolled by two stages, the 16-bit and int8 steady loop by the ring's four.
+        assert stages == (2 if fp8 else 4) and mfmas == stages * (16 if fp8 else 32), (name, mfmas)
+        assert sum("m0" in x for x in loop) == 2 * stages, name
+        assert sum(x == "s_barrier" for x in loop) == stages, name
         assert not any(x.startswith(("scratch_", "buffer_store")) for x in loop), name  # no spills in the loop
+
+
+def issue_cycles(loop: list[str]) -> tuple[int, int]:
+    """A static price of a loop for one wave alone on its SIMD: the wave issues one instruction every 4 cycles, and
+    an MFMA at most every 32 (a 32 x 32 bf16 / int8 MFMA's passes), so the instructions between two MFMAs cost time
+    only past seven. Returns (cycles, the MFMAs' own cycles)."""
+    gaps, cur = [], 0
+    for x in loop:
+        if not x or x.endswith(":"):
+            continue
+        op = x.split()[0]
+        if op.startswith("v_mfma"):
+            gaps.append(cur)
+            cur = 0
+        else:
+            cur += 1 + (int(x.split()[1]) if op == "s_nop" else 0)
+    gaps[0] += cur  # the loop wraps around
+    return sum(max(32, 4 * (g + 1)) for g in gaps), 32 * len(gaps)
+
+
+def test_the_steady_loop_issues_in_the_mfmas_shadow(assembly):
+    """Between two MFMAs a lone wave has seven issue slots; the steady loop's reads, loads, waits and scalar work
+    (the walked buffer resources, placed in slots no read uses) fit in them: the static price is within 1% of the
+    MFMAs' own time for every 16-bit and int8 kernel."""
+    for name, lines in kernels(assembly).items():
+        if "wave8_gemm" in name:
+            continue
+        loops = []
+        for i, line in enumerate(lines):
+            if re.match(r"s_cbranch_scc[01] (\.LBB\S+)", line):
+                start = lines.index(line.split()[-1] + ":")
+                if start < i and any("s_barrier" in x for x in lines[start:i]):
+                    loops.append(lines[start:i + 1])
+        loop = max(loops, key=lambda seg: sum(x.startswith("v_mfma") for x in seg))
+        cycles, ideal = issue_cycles(loop)
+        assert cycles <= 1.01 * ideal, (name, cycles, ideal)
