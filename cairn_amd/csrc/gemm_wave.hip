@@ -24,9 +24,15 @@
 // immediate offset: a write of M0 waits for the wave's previous LDS load to leave the queue, and one per load cost a
 // quarter of the loop (measured). The host runs this kernel only where no lane's offset register would go below zero
 // (Loader::imm_fits).
-// Every iteration issues its loads: past the last stage they read nothing (the buffer resource's range is empty)
-// and land in a buffer no later stage uses, so the loop has no branches and the wait for stage it + 1 is the same
-// count every time. Scheduling fences keep the interleave as written and keep everything on its side of the barrier.
+// Every iteration issues its loads, so the loop has no branches and the wait for stage it + 1 is the same count every
+// time: past the last stage they land in a buffer no later stage reads, from inside the operand's panel or (past its
+// end) as zeros. Iterations come in two forms. Steady ones load stages that end at or before k (and, where k is a
+// whole number of stages, those past the last) with no per-chunk k check; they run STAGES at a time, unrolled, so
+// that each one's ring slot, and with it every LDS address and M0 value, is a constant. The iterations that load the
+// last, partial stage check each chunk against k. The buffer resources are walked a stage at a time by scalar adds
+// (pipe.hpp, Walk) in issue slots no LDS read uses, so that between two MFMAs the wave has no more to issue than the
+// MFMA's 32 cycles take (tests/test_isa.py prices the compiled loop).
+// Scheduling fences keep the interleave as written and keep everything on its side of the barrier.
 // No atomics: the result's bits do not depend on timing.
 #include <hip/hip_runtime.h>
 #include <utility>
