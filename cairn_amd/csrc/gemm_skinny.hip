@@ -14,6 +14,7 @@
 // in LDS and are added in wave order, so two runs give the same bits. The reference has no decode path: its one
 // tiling runs a 1 x n x k call as 64 x 64 tiles (src/cairn/runtime/cairn_tensor.hpp:206-221).
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 #include "kernels.hpp"
@@ -328,6 +329,83 @@ __global__ void __launch_bounds__(256) skinny_rows(Params p, int per_wave) {
   if(r < rows) row(r, xb[0]);
 }
 
+
+// The streaming form, for a few rows of a (m = 2 .. 4 at the decode shape): the matrix core fed straight from
+// global memory, no LDS. A wave owns 16 consecutive rows of b and all of k. Each step of 32 k is one 16-byte load of
+// a (lane l: row l % 16, zero past m; chunk 4 s + l / 16), one of b (row l % 16 of the wave's 16, the same chunk)
+// and one v_mfma_f32_16x16x32_bf16 into the wave's one accumulator. So each b load instruction reads 64 bytes of
+// each of 16 rows: DRAM sees 16 rows streaming side by side, the pattern of the fastest pure read measured on the
+// box. a, at most 16 rows, stays in the caches. D steps make a group; two groups of loads are in flight while the
+// matrix core works through the one before. The accumulator's lane l, value v is row 4 (l / 16) + v of a and row
+// l % 16 of the block; the k order is the matrix core's, step by step, so two runs give the same bits.
+// A workgroup of four waves takes `rows` consecutive rows of b (at most 64; n = 14336: 56, one workgroup a CU).
+template<int D>
+__global__ void __launch_bounds__(256) skinny_stream(Params p, int rows) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = int(blockIdx.x) * rows + 16 * wave;
+  const int left = rows - 16 * wave < p.n - row0 ? rows - 16 * wave : p.n - row0;
+  const int here = left < 16 ? left : 16;  // rows of b this wave holds
+  if(here <= 0) return;
+  const int chunks = p.k / 8;               // 16-byte chunks of a row (k is a multiple of 8)
+  const int whole = chunks / 4, steps = (chunks + 3) / 4;
+  const int r = lane & 15, q = lane >> 4;
+  const __amdgpu_buffer_rsrc_t ra = span(p.a, (std::int64_t(p.m - 1) * p.lda + p.k) * 2);
+  const char* bb = static_cast<const char*>(p.b) + std::int64_t(row0) * p.ldb * 2;
+  const __amdgpu_buffer_rsrc_t rb = span(bb, (std::int64_t(here - 1) * p.ldb + p.k) * 2);
+  // Offsets at step 0; step s adds 64 s. A row past the operand's starts at NOWHERE and stays past every resource.
+  const unsigned a0 = r < p.m ? unsigned(r * p.lda * 2 + q * 16) : unsigned(NOWHERE);
+  const unsigned b0 = r < here ? unsigned(r * p.ldb * 2 + q * 16) : unsigned(NOWHERE);
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  w32x4 xa[2][D], xb[2][D];
+  auto load = [&](int g, w32x4 (&da)[D], w32x4 (&db)[D]) {
+#pragma unroll
+    for(int d = 0; d < D; ++d) {
+      const unsigned at = 64u * unsigned(g * D + d);
+      db[d] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, int(b0 + at), 0, 0));
+      da[d] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, int(a0 + at), 0, 0));
+    }
+  };
+  auto mma = [&](const w32x4 (&da)[D], const w32x4 (&db)[D]) {
+#pragma unroll
+    for(int d = 0; d < D; ++d)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, da[d]), __builtin_bit_cast(bf16x8, db[d]),
+                                                   acc, 0, 0, 0);
+  };
+  const int groups = whole / D;  // groups of D whole steps
+  if(groups > 0) load(0, xa[0], xb[0]);
+  for(int g = 0; g < groups; g += 2) {  // two groups an iteration, so that each buffer is named at compile time
+    if(g + 1 < groups) load(g + 1, xa[1], xb[1]);
+    mma(xa[0], xb[0]);
+    if(g + 2 < groups) load(g + 2, xa[0], xb[0]);
+    if(g + 1 < groups) mma(xa[1], xb[1]);
+  }
+  for(int st = groups * D; st < steps; ++st) {  // the rest one step at a time; chunks past k read zeros
+    const bool in = 4 * st + q < chunks;
+    const unsigned at = 64u * unsigned(st);
+    w32x4 a1[1], b1[1];
+    b1[0] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, in ? int(b0 + at) : NOWHERE, 0, 0));
+    a1[0] = __builtin_bit_cast(w32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, in ? int(a0 + at) : NOWHERE, 0, 0));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1[0]), __builtin_bit_cast(bf16x8, b1[0]),
+                                                 acc, 0, 0, 0);
+  }
+  if(r >= here) return;
+  const int n = row0 + r;
+#pragma unroll
+  for(int v = 0; v < 4; ++v) {
+    const int i = 4 * q + v;
+    if(i >= p.m) continue;
+    float x[1] = {acc[v]};
+    epilogue<1>(p, i, n, x);
+    const std::int64_t o = std::int64_t(i) * p.ldc + n;
+    if(p.c_type == CAIRN_TYPE_F32) {
+      float* out = static_cast<float*>(p.c) + o;
+      *out = p.accumulate ? *out + x[0] : x[0];
+    } else {
+      static_cast<std::uint16_t*>(p.c)[o] = p.c_type == CAIRN_TYPE_BF16 ? narrow_bf16(x[0]) : narrow_f16(x[0]);
+    }
+  }
+}
+
 }  // namespace cairn::gemm
 
 // The width of a workgroup's columns for n: n spread evenly over the 256 CUs, in multiples of 8, from 8 up to the
@@ -339,14 +417,22 @@ int cairn_skinny_width(int n) {
 }
 
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
-  // Three forms, chosen by what measured fastest on the decode shape (n = 14336, k = 4096) in one run of all three:
-  // m = 1, whole rows a wave (5.2 TB/s, against 5.1 for the register form and 4.6 for the ring); m = 5 .. 16 and
-  // n >= 8192, the LDS ring (4.6 against 4.4 TB/s at m = 16); otherwise the register form (m = 2: 4.9 TB/s, where
-  // whole rows are bound by their arithmetic, 4.3; m = 4: 4.6 against 4.5).
+  // Four forms, chosen by what measured fastest on the decode shape (n = 14336, k = 4096) in one run of each set:
+  // m = 1, whole rows a wave (5.2 TB/s, against 5.1 for the register form and 4.6 for the ring); m = 2 .. 4, the
+  // streaming form (m = 4: 5.1 TB/s against 4.6 for the register form); m = 5 .. 16 and n >= 8192, the LDS ring
+  // (4.6 against 4.4 TB/s at m = 16, and 4.0 for the streaming form, whose loads of a's 16 rows double the L2
+  // traffic); otherwise the register form.
   constexpr int ROW_WAVES = 2048;  // 8 a CU
   const int per_wave = (p.n + ROW_WAVES - 1) / ROW_WAVES;
   if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(per_wave) * p.ldb * 2 < 0x7f000000LL) {
     hipLaunchKernelGGL((cairn::gemm::skinny_rows<1, 8>), dim3(unsigned(ROW_WAVES / 4)), dim3(256), 0, s, p, per_wave);
+    return hipGetLastError();
+  }
+  if(p.m >= 2 && p.m <= 4 && p.n >= 2048) {  // rows of b a workgroup: n over the 256 CUs, 16 .. 64
+    const int even = (p.n + 255) / 256;
+    const int rows = std::min(64, std::max(16, (even + 7) / 8 * 8));
+    hipLaunchKernelGGL((cairn::gemm::skinny_stream<8>), dim3(unsigned((p.n + rows - 1) / rows)), dim3(256), 0, s, p,
+                       rows);
     return hipGetLastError();
   }
   if(p.m > 4 && p.n >= 8192) {  // 64 columns a workgroup (16 a wave); 56 a workgroup over all 256 CUs was slower

@@ -347,10 +347,13 @@ def test_skinny_decode_shapes_keep_the_contract(m):
 
 
 # m > 4 with n >= 8192 takes the ring form (64 columns a workgroup, 512-byte stages of k), m = 1 with n >= 2048 and
-# k <= 4096 the row-streaming one (whole rows of b a wave), the rest the register form: tails in each.
+# k <= 4096 the row-streaming one (whole rows of b a wave), m = 2 .. 4 with n >= 2048 the streaming MFMA form (16
+# rows of b a wave; whole groups of 8 steps, then single steps, the last one partial), the rest the register form:
+# tails in each.
 @pytest.mark.parametrize("m,n,k", [(1, 8, 8), (3, 100, 72), (16, 33, 4104), (7, 14336, 24), (5, 200, 4160),
                                    (2, 72, 1000), (3, 8200, 4104), (16, 9000, 520), (1, 8192, 8), (9, 8257, 1032),
-                                   (1, 4100, 4096), (1, 3000, 1000), (1, 20000, 264), (1, 2048, 4088), (5, 8256, 4096)])
+                                   (1, 4100, 4096), (1, 3000, 1000), (1, 20000, 264), (1, 2048, 4088), (5, 8256, 4096),
+                                   (2, 2048, 8), (4, 3001, 1000), (2, 70001, 40), (4, 2050, 520), (3, 14336, 4096)])
 def test_skinny_tails_keep_the_contract(m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = H.normal_bf16(rng, (m, k), 1.0)
@@ -360,6 +363,30 @@ def test_skinny_tails_keep_the_contract(m, n, k):
     assert ch["family"] == "skinny"
     exact, mag = H.exact_product(H.values(L.BF16, a), H.values(L.BF16, b).T)
     assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
+
+
+@pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_RELU])
+def test_every_skinny_form_applies_the_epilogue_in_its_stated_order(act):
+    """Row and column scales, a bf16 bias and an activation on each of the four skinny forms, bf16 out: equal, bit for
+    bit, to the stated steps applied in f32 to what the same form computes without them:
+    bf16(act((f32(acc) * rs[i]) * cs[j] + bias[j]))."""
+    rng = np.random.default_rng(31 + act)
+    for m, n, k in [(1, 4100, 1024), (3, 4100, 1000), (6, 8256, 512), (3, 200, 256)]:  # rows, stream, ring, register
+        a = H.normal_bf16(rng, (m, k), 1.0)
+        b = H.normal_bf16(rng, (n, k), 1.0)
+        rs = rng.uniform(0.25, 2.0, m).astype(np.float32)
+        cs = rng.uniform(0.25, 2.0, n).astype(np.float32)
+        bias = H.normal_bf16(rng, (n,), 4.0)
+        raw, ch = run_gemm(L.BF16, L.F32, m, n, k, a, b, trans_b=True)
+        assert ch["family"] == "skinny"
+        got, _ = run_gemm(L.BF16, L.BF16, m, n, k, a, b, trans_b=True, row_scale=rs, col_scale=cs, bias=bias,
+                          bias_type=L.BF16, act=act)  # fmt: skip
+        v = raw.astype(np.float32) * rs[:, None]
+        v = v * cs[None, :]
+        v = v + H.f32_from_bf16(bias)[None, :]
+        if act == L.ACT_RELU:
+            v = np.where(v < 0, np.float32(0), v)
+        assert np.array_equal(got, H.bf16_from_f32(v)), (m, n, k)
 
 
 # ------------------------------------------------------------------ BASELINE.json's full sizes
