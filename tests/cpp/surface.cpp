@@ -24,7 +24,9 @@ namespace {
 
 struct Log {
   int streams = 0, events = 0, destroyed = 0, records = 0, waits = 0, syncs = 0, mmas = 0, gemms = 0;
+  int allocs = 0, frees = 0, async_allocs = 0, async_frees = 0, event_syncs = 0, lane_runs = 0, library = 0;
   std::vector<int> synced, launched;  // stream ids in order
+  std::vector<std::size_t> sizes;     // bytes of each allocation, in order
 };
 
 // A machine whose streams are small integers; every call is counted.
@@ -42,7 +44,68 @@ struct Recorder {
     ++log->syncs;
     log->synced.push_back(s);
   }
-  void sync_event(Event) noexcept {}
+  void sync_event(Event) noexcept { ++log->event_syncs; }
+  // Memory: host memory stands for device memory, so the operations run their bodies on it.
+  void* alloc(std::size_t b) noexcept {
+    ++log->allocs;
+    log->sizes.push_back(b);
+    return std::malloc(b);
+  }
+  void free(void* p) noexcept {
+    ++log->frees;
+    std::free(p);
+  }
+  void* alloc_async(std::size_t b, Stream) noexcept {
+    ++log->async_allocs;
+    log->sizes.push_back(b);
+    return std::malloc(b);
+  }
+  void free_async(void* p, Stream) noexcept {
+    ++log->async_frees;
+    std::free(p);
+  }
+  void copy(void* dst, const void* src, std::size_t b, cr::reuse::Dir, Stream) noexcept { std::memcpy(dst, src, b); }
+  // The lane and library primitives, run at once on the host: body(i) for every i; a fold, an inclusive scan and an
+  // exclusive sum that, asked with null storage, say they need a few bytes of it.
+  template<unsigned U, class F> void lanes(std::size_t n, const F& body, Stream, unsigned, std::size_t) noexcept {
+    ++log->lane_runs;
+    for(std::size_t i = 0; i < n; ++i) body(i);
+  }
+  template<class In, class Out, class Fold, class T>
+  void reduce(void* temp, std::size_t& bytes, In in, Out out, std::size_t n, Fold fold, T identity, Stream) noexcept {
+    if(!temp) {
+      bytes = 96;
+      return;
+    }
+    ++log->library;
+    T acc = identity;
+    for(std::size_t i = 0; i < n; ++i) acc = fold(acc, in[i]);
+    *out = acc;
+  }
+  template<class In, class Out, class Fold>
+  void inclusive_scan(void* temp, std::size_t& bytes, In in, Out out, Fold fold, std::size_t n, Stream) noexcept {
+    if(!temp) {
+      bytes = 40;
+      return;
+    }
+    ++log->library;
+    auto acc = in[0];
+    out[0] = acc;
+    for(std::size_t i = 1; i < n; ++i) out[i] = acc = fold(acc, in[i]);
+  }
+  template<class In, class Out>
+  void exclusive_sum(void* temp, std::size_t& bytes, In in, Out out, std::size_t n, Stream) noexcept {
+    if(!temp) {
+      bytes = 24;
+      return;
+    }
+    ++log->library;
+    std::size_t acc = 0;
+    for(std::size_t i = 0; i < n; ++i) {
+      out[i] = acc;
+      acc += in[i];
+    }
+  }
   // The device multiply, run at once on the host arrays: its results are the reference loop's.
   void mma(int type, std::size_t m, std::size_t n, std::size_t k, float* c, const void* a, const void* b,
            Stream s) noexcept {
@@ -159,6 +222,94 @@ int context() {
     cr::tensor::gemm(ctx, d);
     expect(log.gemms == 1 && log.syncs == 1, "gemm is synchronous work on the lane");
   }
+  {  // the arena: a reserve allocated up front and never again within it; each user waits for the last one
+    Log log;
+    {
+      Ctx ctx(cr::reuse::Budget{1024, 4096}, cr::reuse::Allocation::synchronous, Recorder{&log});
+      expect(log.allocs == 1 && ctx.capacity() == 1024, "a budget's reserve is allocated when the context is made");
+      auto* lane = ctx.lend(true);
+      void* p = nullptr;
+      expect(ctx.acquire(512, *lane, &p) == cr::reuse::Scratch::ok && p && log.allocs == 1 && log.waits == 0,
+             "scratch within the reserve allocates nothing, and the first user waits for no one");
+      ctx.release(*lane);
+      void* q = nullptr;
+      expect(ctx.acquire(800, *lane, &q) == cr::reuse::Scratch::ok && q == p && log.waits == 1,
+             "the next user's stream waits on the event the last one's release recorded");
+      ctx.release(*lane);
+      const int syncs = log.event_syncs;
+      expect(ctx.acquire(2000, *lane, &q) == cr::reuse::Scratch::ok && ctx.grown() == 1 && log.frees == 1 &&
+                 log.allocs == 2 && log.sizes.back() == 2000 && log.event_syncs == syncs + 1 && log.waits == 1,
+             "growth within the limit waits for the last user, frees, allocates, and owes the new storage no wait");
+      ctx.release(*lane);
+      void* r = nullptr;
+      expect(ctx.acquire(5000, *lane, &r) == cr::reuse::Scratch::over_budget && r == nullptr && log.allocs == 2 &&
+                 ctx.capacity() == 2000,
+             "past the limit the answer is over_budget and nothing changes");
+      expect(ctx.acquire(100, *lane, &r) == cr::reuse::Scratch::ok, "and the arena is still free to lease");
+      ctx.release(*lane);
+      ctx.give_back(lane);
+    }
+    expect(log.frees == 2 && log.event_syncs >= 2, "the context's end waits for the arena's last user, then frees it");
+  }
+  {  // stream-ordered growth: the host never waits, the old storage goes on the lane's stream
+    Log log;
+    Ctx ctx(cr::reuse::Budget{0, cr::reuse::UNBOUNDED}, cr::reuse::Allocation::stream_ordered, Recorder{&log});
+    auto* lane = ctx.lend(true);
+    void* p = nullptr;
+    ctx.acquire(100, *lane, &p);
+    ctx.release(*lane);
+    ctx.acquire(300, *lane, &p);
+    ctx.release(*lane);
+    expect(log.async_allocs == 2 && log.async_frees == 1 && log.allocs == 0 && log.event_syncs == 0,
+           "stream-ordered growth allocates and frees on the stream and never stops the host");
+    ctx.give_back(lane);
+  }
+  {  // the operations on the arena: their results, and nothing allocated after the first
+    Log log;
+    Ctx ctx(Recorder{&log});
+    long long total = 0;
+    auto value = [](std::size_t i) { return (long long)(i); };
+    auto add = [](long long x, long long y) { return x + y; };
+    const bool r1 = cr::reuse::reduce(ctx, total, 100, 0LL, add, value) == cr::reuse::Scratch::ok && total == 4950;
+    const int allocs = log.allocs;
+    long long again = 0;
+    cr::reuse::reduce(ctx, again, 100, 0LL, add, value);
+    expect(r1 && again == 4950 && log.allocs == allocs, "a reduce's result, and the arena kept for the next one");
+    std::vector<long long> inc(10), exc(10);
+    long long t1 = 0, t2 = 0;
+    cr::reuse::scan<false>(ctx, t1, inc.data(), 10, 0LL, add, value);
+    cr::reuse::scan<true>(ctx, t2, exc.data(), 10, 0LL, add, value);
+    bool sc = t1 == 45 && t2 == 45;
+    for(std::size_t i = 0; i < 10; ++i)
+      sc &= inc[i] == (long long)(i * (i + 1) / 2) && exc[i] == (long long)(i ? i * (i - 1) / 2 : 0);
+    expect(sc, "inclusive and exclusive scans, with the total");
+    std::vector<int> out(50, -1);
+    std::size_t used = 0;
+    cr::reuse::compact(ctx, &used, out.data(), 100, [](std::size_t i) { return i % 2 == 0; },
+                       [](std::size_t i) { return int(10 * i); });
+    bool cp = used == 50;
+    for(std::size_t j = 0; j < 50; ++j) cp &= out[j] == int(20 * j);
+    expect(cp, "a compaction keeps the selected values in order and counts them");
+    long long sunk = -1;
+    cr::reuse::reduce_into(ctx, &sunk, 5, 0LL, add, value);
+    expect(sunk == 10, "reduce_into leaves the total where the device reads it");
+    Ctx tight(cr::reuse::Budget{0, 0}, cr::reuse::Allocation::synchronous, Recorder{&log});
+    long long untouched = 7;
+    expect(cr::reuse::reduce(tight, untouched, 10, 0LL, add, value) == cr::reuse::Scratch::over_budget &&
+               untouched == 7 && tight.lent() == 0,
+           "over budget, a reduce queues nothing, leaves its result, and gives its lane back");
+  }
+  {  // tickets: a lent lane for queued work, ordered after another, handed back by its one wait
+    Log log;
+    Ctx ctx(Recorder{&log});
+    cr::reuse::Lent<Recorder> first(ctx);
+    cr::reuse::Lent<Recorder> second(ctx);
+    second.follow(first.mark());
+    expect(ctx.lent() == 2 && first.stream() != second.stream() && log.waits == 1, "two tickets, two lanes, one ordered");
+    std::move(second).wait();
+    std::move(first).wait();
+    expect(ctx.lent() == 0 && ctx.streams_made() == 2, "each wait hands its lane back");
+  }
   {  // a second lane while a run is held starts after the held work
     Log log;
     Ctx ctx(Recorder{&log});
@@ -192,6 +343,16 @@ int trap_case(const std::string& which) {
   } else if(which == "leaked") {
     ctx->lend();
     delete ctx;  // a lane never given back
+  } else if(which == "lease") {  // the arena leased twice
+    auto* lane = ctx->lend(true);
+    void* p = nullptr;
+    ctx->acquire(16, *lane, &p);
+    ctx->acquire(16, *lane, &p);
+  } else if(which == "unleased") {  // released with no lease
+    auto* lane = ctx->lend(true);
+    ctx->release(*lane);
+  } else if(which == "ticket") {  // a ticket dropped unawaited
+    cr::reuse::Lent<Recorder> t(*ctx);
   } else if(which == "overflow") (void)cr::mul<std::size_t>(std::size_t(1) << 40, std::size_t(1) << 40);
   else if(which == "e4m3") (void)cr::fp::narrow<cr::f8e4m3>(465.0);
   else if(which == "scale") (void)cr::fp::quantize<cr::bf16>(1.0f, 0.0f);

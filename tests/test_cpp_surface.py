@@ -32,10 +32,11 @@ def test_the_context_keeps_the_reference_rules(surface):
     done = run(surface, "context")
     assert done.returncode == 0, done.stdout + done.stderr
     lines = done.stdout.splitlines()
-    assert lines[-1] == "0 failures" and sum(line.startswith("ok ") for line in lines) >= 17
+    assert lines[-1] == "0 failures" and sum(line.startswith("ok ") for line in lines) >= 30
 
 
-@pytest.mark.parametrize("case", ["shape", "nested", "settle", "observe", "leaked", "overflow", "e4m3", "scale"])
+@pytest.mark.parametrize("case", ["shape", "nested", "settle", "observe", "leaked", "lease", "unleased", "ticket",
+                                  "overflow", "e4m3", "scale"])
 def test_misuse_traps(surface, case):
     done = run(surface, "trap", case)
     assert done.returncode == -6 and "returned" not in done.stdout, (done.returncode, done.stdout)
