@@ -443,20 +443,28 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   const int T = (p.k + Sh::BK - 1) / Sh::BK;
   using LA = Loader<Sh, Sh::BM, AK, Dma>;
   using LB = Loader<Sh, Sh::BN, BKM, Dma>;
-  auto at_of = [&](int st) { return ring + unsigned((st % S) * Sh::STAGE); };
-  auto load_a = [&](const auto& r, int st, auto u) {
-    if constexpr(decltype(u)::value == 0) dma.set_base(LA::base(at_of(st), wave));
-    la.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  // A stage's place in the ring (a constant in the unrolled steady loop, else an int), and one operand's part of stage
+  // st there: M0 once, then its loads by immediate offset, each chunk checked against k only with `tail`.
+  using Tail = std::true_type;
+  using Steady = std::false_type;
+  auto stage_at = [&](auto slot) { return lds + int(slot) * Sh::STAGE; };
+  auto load_a = [&](const auto& r, int st, auto slot, auto u, auto tail) {
+    constexpr int U = decltype(u)::value;
+    if constexpr(U == 0) dma.set_base(LA::base(ring + unsigned(int(slot) * Sh::STAGE), wave));
+    if constexpr(decltype(tail)::value) la.template load_imm<U>(dma, r, st, p.k);
+    else la.template load_steady<U>(dma, r);
   };
-  auto load_b = [&](const auto& r, int st, auto u) {
-    if constexpr(decltype(u)::value == 0) dma.set_base(LB::base(at_of(st) + Sh::A_BYTES, wave));
-    lb.template load_imm<decltype(u)::value>(dma, r, st, p.k);
+  auto load_b = [&](const auto& r, int st, auto slot, auto u, auto tail) {
+    constexpr int U = decltype(u)::value;
+    if constexpr(U == 0) dma.set_base(LB::base(ring + unsigned(int(slot) * Sh::STAGE + Sh::A_BYTES), wave));
+    if constexpr(decltype(tail)::value) lb.template load_imm<U>(dma, r, st, p.k);
+    else lb.template load_steady<U>(dma, r);
   };
   auto stage_all = [&](int st) {
     const auto ra = la.resource(dma, a, pa.bytes, p.lda, st);
-    unrolled<Sh::LOADS_A>([&](auto u) { load_a(ra, st, u); });
+    unrolled<Sh::LOADS_A>([&](auto u) { load_a(ra, st, st % S, u, Tail{}); });
     const auto rb = lb.resource(dma, b, pb.bytes, p.ldb, st);
-    unrolled<Sh::LOADS_B>([&](auto u) { load_b(rb, st, u); });
+    unrolled<Sh::LOADS_B>([&](auto u) { load_b(rb, st, st % S, u, Tail{}); });
   };
 
   Acc acc[FM][FN];
@@ -465,13 +473,18 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
 #pragma unroll
     for(int j = 0; j < FN; ++j) acc[i][j] = Acc{};
   u32x4 xa[2][2][FM], xb[2][2][FN];  // [buffer][k-step of the stage][block]
+  int ta_off[FM], tb_off[FN];        // transpose-read offsets at k-step 0, half 0 (mnmajor_step adds the rest)
+#pragma unroll
+  for(int i = 0; i < FM; ++i) ta_off[i] = AK ? 0 : mnmajor_fragment<ES, Sh::BM>(wr + 32 * i, 0, 0, lane);
+#pragma unroll
+  for(int j = 0; j < FN; ++j) tb_off[j] = BKM ? 0 : mnmajor_fragment<ES, Sh::BN>(wc + 32 * j, 0, 0, lane);
   // Read X of a stage's READS: k-step X / STEP_READS, then as wave_gemm orders a k-step's reads.
   auto read = [&](auto buf, const char* stage, auto x) {
     constexpr int BUF = decltype(buf)::value, X = decltype(x)::value % STEP_READS, s = decltype(x)::value / STEP_READS;
     if constexpr(X < RA) {
       if constexpr(AK) xa[BUF][s][X] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(wr + 32 * X, s, lane));
       else {
-        const u32x2 h = transpose_half<ES>(stage + mnmajor_fragment<ES, Sh::BM>(wr + 32 * (X / 2), s, X % 2, lane));
+        const u32x2 h = transpose_half<ES>(stage + ta_off[X / 2] + mnmajor_step<ES, Sh::BM>(s, X % 2));
         xa[BUF][s][X / 2][2 * (X % 2)] = h[0];
         xa[BUF][s][X / 2][2 * (X % 2) + 1] = h[1];
       }
@@ -480,7 +493,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
       const char* bs = stage + Sh::A_BYTES;
       if constexpr(BKM) xb[BUF][s][Y] = *reinterpret_cast<const u32x4*>(bs + kmajor_fragment(wc + 32 * Y, s, lane));
       else {
-        const u32x2 h = transpose_half<ES>(bs + mnmajor_fragment<ES, Sh::BN>(wc + 32 * (Y / 2), s, Y % 2, lane));
+        const u32x2 h = transpose_half<ES>(bs + tb_off[Y / 2] + mnmajor_step<ES, Sh::BN>(s, Y % 2));
         xb[BUF][s][Y / 2][2 * (Y % 2)] = h[0];
         xb[BUF][s][Y / 2][2 * (Y % 2) + 1] = h[1];
       }
@@ -490,20 +503,31 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
     constexpr int BUF = decltype(buf)::value, I = decltype(x)::value / FN, J = decltype(x)::value % FN;
     acc[I][J] = M::step(xb[BUF][0][J], xb[BUF][1][J], xa[BUF][0][I], xa[BUF][1][I], acc[I][J]);
   };
-  auto stage_of = [&](int st) { return lds + (st % S) * Sh::STAGE; };
-
   // Stages 0 .. S - 1 (every buffer starts free), then stage 0's fragments.
   for(int st = 0; st < S; ++st) stage_all(st);
   wait_loads<(S - 1) * LOADS>();
   fenced_barrier();
-  unrolled<READS>([&](auto x) { read(std::integral_constant<int, 0>{}, stage_of(0), x); });
+  unrolled<READS>([&](auto x) { read(std::integral_constant<int, 0>{}, stage_at(std::integral_constant<int, 0>{}), x); });
 
-  auto iteration = [&](int it, auto cur) {
+  // Iteration `it` loads stage it + S into the slot stage it leaves. Its resources are walked a stage at a time and
+  // made after MFMAs 12 .. 15 of the iteration before, slots no load uses; steady iterations (stages that end
+  // at or before k, or past the last where k is whole stages) skip the per-chunk k check.
+  Walk wa = walk<Sh, AK>(a, pa.bytes, p.lda, S), wb = walk<Sh, BKM>(b, pb.bytes, p.ldb, S);
+  Dma::Rsrc ra = Dma::resource(wa), rb = Dma::resource(wb);
+  wa.advance();
+  wb.advance();
+  unsigned records;
+  const int steady = p.k % Sh::BK == 0 ? T : (T - 1 - S > 0 ? T - 1 - S : 0);
+  // A 32x32x64 fp8 MFMA takes 64 cycles: between two, fifteen issue slots, room for two reads and the walk's work.
+  static_assert(8 + Sh::LOADS_B <= 12, "MFMAs 12 .. 15 of a stage issue no load");
+  auto iteration = [&](int it, auto slot, auto cur, auto tail) {
     constexpr int C = decltype(cur)::value, N = 1 - C;
-    const int sl = it + S;  // the stage whose loads this iteration issues, into stage it's buffer
-    const auto ra = la.resource(dma, a, pa.bytes, p.lda, sl);
-    const auto rb = lb.resource(dma, b, pb.bytes, p.ldb, sl);
-    const char* nxt = stage_of(it + 1);
+    const auto next = [&] {
+      if constexpr(std::is_integral_v<decltype(slot)>) return (slot + 1) % S;
+      else return std::integral_constant<int, (decltype(slot)::value + 1) % S>{};
+    }();
+    const int sl = it + S;  // the stage whose loads this iteration issues, into stage it's slot
+    const char* nxt = stage_at(next);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wait_loads<(S - 2) * LOADS>();
     fenced_barrier();
@@ -513,17 +537,33 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
       fence();
       if constexpr(2 * X < READS) read(std::integral_constant<int, N>{}, nxt, std::integral_constant<int, 2 * X>{});
       if constexpr(2 * X + 1 < READS) read(std::integral_constant<int, N>{}, nxt, std::integral_constant<int, 2 * X + 1>{});
-      if constexpr(X >= 4 && X < 4 + Sh::LOADS_A) load_a(ra, sl, std::integral_constant<int, X - 4>{});
-      if constexpr(X >= 8 && X < 8 + Sh::LOADS_B) load_b(rb, sl, std::integral_constant<int, X - 8>{});
+      if constexpr(X >= 4 && X < 4 + Sh::LOADS_A) load_a(ra, sl, slot, std::integral_constant<int, X - 4>{}, tail);
+      if constexpr(X >= 8 && X < 8 + Sh::LOADS_B) load_b(rb, sl, slot, std::integral_constant<int, X - 8>{}, tail);
+      if constexpr(X == 12) records = wa.records();
+      if constexpr(X == 13) {
+        ra = Dma::resource(wa.at, records);
+        wa.advance();
+        pin(wa);
+      }
+      if constexpr(X == 14) records = wb.records();
+      if constexpr(X == 15) {
+        rb = Dma::resource(wb.at, records);
+        wb.advance();
+        pin(wb);
+      }
       fence();
     });
   };
+  // Steady iterations S at a time (S is even, so each one's register buffer and ring slot are constants), then the
+  // rest one at a time.
+  static_assert(S % 2 == 0, "the register buffers alternate within an unrolled group");
   int it = 0;
-  for(; it + 1 < T; it += 2) {
-    iteration(it, std::integral_constant<int, 0>{});
-    iteration(it + 1, std::integral_constant<int, 1>{});
+  for(; it + S <= steady; it += S)
+    unrolled<S>([&](auto u) { iteration(it + decltype(u)::value, u, std::integral_constant<int, decltype(u)::value % 2>{}, Steady{}); });
+  for(; it < T; ++it) {
+    if(it & 1) iteration(it, it % S, std::integral_constant<int, 1>{}, Tail{});
+    else iteration(it, it % S, std::integral_constant<int, 0>{}, Tail{});
   }
-  if(it < T) iteration(it, std::integral_constant<int, 0>{});
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
   store_tile<Sh, false>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
 }
