@@ -419,7 +419,8 @@ int cairn_skinny_width(int n) {
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // Four forms, chosen by what measured fastest on the decode shape (n = 14336, k = 4096) in one run of each set:
   // m = 1, whole rows a wave (5.2 TB/s, against 5.1 for the register form and 4.6 for the ring); m = 2 .. 4, the
-  // streaming form (m = 4: 5.1 TB/s against 4.6 for the register form); m = 5 .. 16 and n >= 8192, the LDS ring
+  // streaming form (side by side in one process: m = 4 4.76 against 4.58 TB/s for the register form, m = 3 4.85
+  // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 8192, the LDS ring
   // (4.6 against 4.4 TB/s at m = 16, and 4.0 for the streaming form, whose loads of a's 16 rows double the L2
   // traffic); otherwise the register form.
   constexpr int ROW_WAVES = 2048;  // 8 a CU
