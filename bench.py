@@ -348,10 +348,39 @@ def cpu_baseline(seconds: float = 12.0) -> dict | None:
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     tflops = 2.0 * n**3 / med / 1e12
-    return {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": kind,
-            "sample": f"bf16 {n}^3 c += a.b, single thread, {len(times)} calls over ~{seconds:.0f} s, median",
-            "ms_per_call": med * 1e3, "extrapolated_4096_cubed_s": med * (4096 / n) ** 3,
-            "host_cpus": os.cpu_count()}  # fmt: skip
+    out = {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": kind,
+           "sample": f"bf16 {n}^3 c += a.b, single thread, {len(times)} calls over ~{seconds:.0f} s, median",
+           "ms_per_call": med * 1e3, "extrapolated_4096_cubed_s": med * (4096 / n) ** 3,
+           "host_cpus": os.cpu_count()}  # fmt: skip
+    out["c1"] = cpu_c1(lib, kind)
+    return out
+
+
+def cpu_c1(lib: C.CDLL, kind: str, n: int = 512, calls: int = 5) -> dict:
+    """C1: the f32 512^3 host multiply (the reference's multiply<float>, or the oracle's restatement), single
+    thread, a ~ U[-1, 1), c = 0, median of `calls` calls, in GFLOP/s. The one configuration the reference runs
+    on the CPU alone; it has no GPU roofline."""
+    P = C.c_void_p
+    rng = np.random.default_rng(512)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    c = np.zeros((n, n), dtype=np.float32)
+    if kind == "reference":
+        f = lib.ref_mma_f32
+        f.argtypes = [C.c_size_t] * 3 + [P, C.c_size_t, P, C.c_size_t, P, C.c_size_t]
+        call = lambda: f(n, n, n, c.ctypes.data_as(P), n * n, a.ctypes.data_as(P), n * n, b.ctypes.data_as(P), n * n)
+    else:
+        f = lib.oracle_mma
+        f.argtypes = [C.c_int] + [C.c_size_t] * 3 + [P, C.c_size_t, P, C.c_size_t, P, C.c_size_t]
+        call = lambda: f(0, n, n, n, c.ctypes.data_as(P), n * n, a.ctypes.data_as(P), n * n, b.ctypes.data_as(P), n * n)
+    times = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": 2.0 * n**3 / med / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": kind,
+            "sample": f"f32 {n}^3 c += a.b, single thread, median of {calls} calls", "ms_per_call": med * 1e3}
 
 
 def main() -> int:
