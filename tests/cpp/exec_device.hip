@@ -157,3 +157,39 @@ extern "C" int exec_owners(int* out, unsigned char* bytes) {
   copy_on(ctx, bytes, pz, 37, Dir::d2h);
   return 0;
 }
+
+// The device-resident forms: reduce_to after a ticket (its total read after the ticket's wait), reduce_into and
+// scan_into inside a held run (nothing waits until the run ends), a vector plan given a pointer off its chunk's
+// width (the scalar lanes run instead), and a region of no indices. out: [reduce_to, reduce_into, exclusive scan
+// of 0 .. 9 (10 values), vector plan over n floats from an odd float offset (n values)].
+extern "C" int exec_resident(std::size_t n, long long* out, float* vec) {
+  Context& ctx = here();
+  Buffer<long long> cells(2), prefix(10);
+  Buffer<float> v(n + 1);
+  long long* pc = cells.data();
+  Lent fill = queue(ctx, 2, [=] __device__(std::size_t i) { pc[i] = -1; });
+  Scratch answer = Scratch::over_budget;
+  Lent total = reduce_to(ctx, pc, 1000, 0LL, Add{}, [] __host__ __device__(std::size_t i) { return (long long)i; },
+                         &answer, fill);
+  wait(std::move(total));
+  wait(std::move(fill));
+  if(answer != Scratch::ok) return 1;
+  {
+    Held held;
+    reduce_into(ctx, pc + 1, 100, 0LL, Add{}, [] __host__ __device__(std::size_t i) { return (long long)(2 * i); });
+    scan_into<true>(ctx, prefix.data(), 10, 0LL, Add{}, [] __host__ __device__(std::size_t i) { return (long long)i; });
+  }
+  copy_on(ctx, out, pc, 2, Dir::d2h);
+  copy_on(ctx, out + 2, prefix.data(), 10, Dir::d2h);
+  float* odd = v.data() + 1;  // 4 bytes past a 256-byte boundary: not on a 16-byte chunk
+  run_vector<4>(
+      ctx, n, aligned<4>(odd), [=] __device__(std::size_t i) { odd[i] = 3.0f * float(i); },
+      [=] __device__(std::size_t i) {
+        Chunk<float, 4> c;
+        for(unsigned e = 0; e < 4; ++e) c[e] = -1.0f;  // never taken for this pointer
+        c.store(odd + i);
+      });
+  run(ctx, 0, [=] __device__(std::size_t i) { odd[i] = -7.0f; });  // no indices: nothing runs
+  copy_on(ctx, vec, odd, n, Dir::d2h);
+  return aligned<4>(odd) ? 2 : 0;
+}

@@ -31,7 +31,8 @@ def ex():
     lib.exec_queue.argtypes = [C.c_size_t, P]
     lib.exec_budget.argtypes = [C.c_size_t, C.c_size_t, P, P, P]
     lib.exec_owners.argtypes = [P, P]
-    for f in (lib.exec_regions, lib.exec_streams, lib.exec_queue, lib.exec_budget, lib.exec_owners):
+    lib.exec_resident.argtypes = [C.c_size_t, P, P]
+    for f in (lib.exec_regions, lib.exec_streams, lib.exec_queue, lib.exec_budget, lib.exec_owners, lib.exec_resident):
         f.restype = C.c_int
     return lib
 
@@ -102,3 +103,14 @@ def test_owners_and_zeroing(ex):
     if out[0] == -1:
         pytest.skip("the device reports no coherent access to managed memory: the unified owner is not exercised")
     assert np.array_equal(out, np.arange(16) ** 2)
+
+
+def test_device_resident_results_and_the_scalar_fallback(ex):
+    n = 1003
+    out = np.zeros(12, np.int64)
+    vec = np.zeros(n, np.float32)
+    assert ex.exec_resident(n, ptr(out), ptr(vec)) == 0
+    assert out[0] == 499500  # reduce_to, read after its ticket's wait
+    assert out[1] == 2 * 4950  # reduce_into inside a held run
+    assert np.array_equal(out[2:], np.concatenate([[0], np.cumsum(np.arange(9))]))  # scan_into, exclusive
+    assert np.array_equal(vec, 3.0 * np.arange(n, dtype=np.float32))  # the scalar lanes, and the empty region left it
