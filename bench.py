@@ -4,7 +4,9 @@ bf16 output) with int8 TOPS (W8A8, fused dequant to bf16), as a fraction of the 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
 A step is one 4096^3 bf16 GEMM on inputs already resident in HBM. W untimed steps, then exactly K timed steps between
-two synchronizations; `value` is 2 * 4096^3 * K / wall seconds. The same run also measures, as extra records:
+two synchronizations; `value` is 2 * 4096^3 * K / wall seconds. The default W (400, about 45 ms of the 4096^3 GEMM)
+outlasts the clock ramp of a GPU coming out of idle: after half a second idle, the first 50 launches of the 4096^3
+GEMM average 255 us, launches 100-149 113 us, and from about launch 300 on it holds 109 us. The same run also measures, as extra records:
 int8 W8A8 4096^3 TOPS; f8e4m3 4096^3 on the fp8 matrix core; the skinny decode GEMMs (m = 1, 4, 16; n = 14336; k = 4096; b stored n x k) in HBM GB/s,
 rotating enough copies of b that the 256 MB MALL cannot hold them; the MLP forward + backward (3 GEMMs); the
 bf16 -> int8 activation quantize in HBM GB/s; and the reference's CPU loop timed on this host (cpu_baseline).
@@ -291,21 +293,26 @@ def measured_traffic(kernel: str) -> dict | None:
     return None
 
 
-def summarize(directory: Path) -> None:
+def summarize(directory: Path, last: int) -> None:
     """Tables from rocprofv3's CSV output in `directory` (--output-format csv): per kernel and grid, the launch count
-    and durations from *_kernel_trace.csv; per dispatch, the counter readings from *_counter_collection.csv."""
+    and durations from *_kernel_trace.csv, with the average of the last `last` launches (a bench section's timed
+    steps, after its warm-up); per dispatch, the counter readings from *_counter_collection.csv."""
     import csv
 
     for path in sorted(directory.glob("*_kernel_trace.csv")):
-        groups: dict[tuple, list[int]] = {}
+        groups: dict[tuple, list[tuple[int, int]]] = {}
         for r in csv.DictReader(path.open()):
             key = (r["Kernel_Name"], int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
-            groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
-        print(f"{path.name}: kernel | grid (threads) | launches | average us | median us | min us")
-        for (name, grid), ns in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-            ns.sort()
-            print(f"{name} | {grid} | {len(ns)} | {sum(ns) / len(ns) / 1e3:.1f} | {ns[len(ns) // 2] / 1e3:.1f} | "
-                  f"{ns[0] / 1e3:.1f}")  # fmt: skip
+            start = int(r["Start_Timestamp"])
+            groups.setdefault(key, []).append((start, int(r["End_Timestamp"]) - start))
+        print(f"{path.name}: kernel | grid (threads) | launches | average us | average of the last {last} us | "
+              f"median us | min us")  # fmt: skip
+        for (name, grid), runs in sorted(groups.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+            runs.sort()
+            tail = [d for _, d in runs[-last:]]
+            ns = sorted(d for _, d in runs)
+            print(f"{name} | {grid} | {len(ns)} | {sum(ns) / len(ns) / 1e3:.1f} | {sum(tail) / len(tail) / 1e3:.1f} | "
+                  f"{ns[len(ns) // 2] / 1e3:.1f} | {ns[0] / 1e3:.1f}")  # fmt: skip
     for path in sorted(directory.glob("*_counter_collection.csv")):
         print(f"{path.name}: dispatch | kernel | grid (threads) | counter | value (KiB) | duration us")
         for r in csv.DictReader(path.open()):
@@ -387,14 +394,14 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--only", choices=["square", "skinny", "mlp", "quantize", "all", "traffic", "calibrate"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--family", choices=["pipe", "wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
     args = ap.parse_args()
     if args.summarize:
-        summarize(args.summarize)
+        summarize(args.summarize, args.steps)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",

@@ -161,6 +161,9 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
           }
         });
       }
+      // The rows go out as non-temporal stores: c is written once and not read again by this launch, and streaming it
+      // past L2 leaves less to write back when the launch ends (4096^3: 0.5-1 us of 105 bf16, 0.7 of 63 int8 W8A8,
+      // side by side against plain stores).
       const int cl = lane & 15;
       char* out = static_cast<char*>(p.c) + (std::int64_t(row0 + wr) * p.ldc + col0 + wc) * 2 + 16 * cl;
 #pragma unroll
@@ -168,7 +171,7 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
         const int r = 4 * s + (lane >> 4);
         u32x4 v = *reinterpret_cast<const u32x4*>(mine + r * 256 + 16 * (cl ^ ((r & 31) >> 1)));
         if(r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
-        *reinterpret_cast<u32x4*>(out + std::int64_t(r) * p.ldc * 2) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out + std::int64_t(r) * p.ldc * 2));
       }
       return;
     }
