@@ -6,8 +6,11 @@
 // quantizes a row of up to 4096 elements (four rows a workgroup), a workgroup a longer one. Each lane holds 8-element
 // chunks of the row in registers, so with a computed scale the row is read once: the largest magnitude is reduced
 // across the wave (and the workgroup), the scale follows, and the held chunks are quantized. Rows longer than the
-// chunks held (8192 elements for a workgroup) are read twice, the second time from cache. The element arithmetic is quantize.hpp's: an f32 shortcut where it decides, the reference's double
-// steps where it does not, so every output equals the reference's.
+// chunks held (8192 elements for a workgroup) are read twice, the second time from cache. The element arithmetic is
+// quantize.hpp's, so every output equals the reference's: for int8 an f32 shortcut where it decides and the
+// reference's double steps where it does not; for the 8-bit floats the hardware's conversion, with elements near a
+// midpoint of the grid settled from the neighbouring codes (convert_f8), and the integer steps for saturation and
+// special values.
 #include <hip/hip_runtime.h>
 #include "../../include/cairn_gemm.h"
 #include "quantize.hpp"
@@ -317,6 +320,31 @@ __device__ __forceinline__ u32x2 pack_i8(const int (&c)[CHUNK]) {
   return o;
 }
 
+// A chunk into the 8-bit float QT through the hardware's conversions, four codes a word (convert_f8 in quantize.hpp
+// states when its answer is the reference's).
+template<int QT> __device__ __forceinline__ bool hw_f8(const float (&x)[CHUNK], const float (&y)[CHUNK], float s,
+                                                       u32x2& o) {
+  using T = std::conditional_t<QT == CAIRN_TYPE_F8E4M3, cr::f8e4m3, cr::f8e5m2>;
+  std::uint32_t w[2];
+  const bool ok = convert_f8<T>(
+      x, y, s, w,
+      [](float a, float b, float c, float d) {
+        if constexpr(QT == CAIRN_TYPE_F8E4M3)
+          return std::uint32_t(
+              __builtin_amdgcn_cvt_pk_fp8_f32(c, d, __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false), true));
+        else
+          return std::uint32_t(
+              __builtin_amdgcn_cvt_pk_bf8_f32(c, d, __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false), true));
+      },
+      [](std::uint32_t code) {
+        if constexpr(QT == CAIRN_TYPE_F8E4M3) return __builtin_amdgcn_cvt_f32_fp8(int(code), 0);
+        else return __builtin_amdgcn_cvt_f32_bf8(int(code), 0);
+      });
+  o[0] = w[0];
+  o[1] = w[1];
+  return ok;
+}
+
 template<int XT, int QT, int ROWS>
 __global__ void __launch_bounds__(THREADS) quantize_fast(Params p) {
   constexpr int RT = THREADS / ROWS, HOLD = ROWS == 1 ? 4 : 8;
@@ -406,25 +434,20 @@ __global__ void __launch_bounds__(THREADS) quantize_fast(Params p) {
         o = pack_i8(c);
       } else {
         using T = std::conditional_t<QT == CAIRN_TYPE_F8E4M3, cr::f8e4m3, cr::f8e5m2>;
-        std::uint32_t b[CHUNK];
-        bool any = false;
-        bool need[CHUNK];
+        float x[CHUNK], y[CHUNK];
 #pragma unroll
         for(int e = 0; e < CHUNK; ++e) {
-          const float x = element<XT>(w[j], e);
-          need[e] = !try_f8<T>(x, x * r, b[e]);
-          any |= need[e];
+          x[e] = element<XT>(w[j], e);
+          y[e] = x[e] * r;
         }
-        if(any) {
+        if(!hw_f8<QT>(x, y, s, o)) {  // saturation, infinity, NaN: rare; the integer steps decide
+          std::uint32_t b[CHUNK];
 #pragma unroll
           for(int e = 0; e < CHUNK; ++e)
-            if(need[e]) {
-              const float x = element<XT>(w[j], e);
-              b[e] = near_f8<T>(x, s, x * r);
-            }
+            if(!try_f8<T>(x[e], y[e], b[e])) b[e] = near_f8<T>(x[e], s, y[e]);
+          o[0] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+          o[1] = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
         }
-        o[0] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-        o[1] = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
       }
       __builtin_amdgcn_raw_buffer_store_b64(o, qs, int(col_of(base, j)), 0, 0);
     }

@@ -169,6 +169,58 @@ template<class T> CR_HD inline std::uint32_t near_f8(float x, float s, float y) 
 // stay finite in near_f8.
 CR_HD inline bool fast_ok_f8(float s) { return s >= 0x1p-100f && s <= 0x1p100f; }
 
+// Eight elements x into T, given y = x * (1 / s), through a round-to-nearest-even conversion `word` (four f32 to
+// four codes in one word, low byte first) that does not saturate, and its exact inverse `decode` (a code's magnitude
+// bits to f32). The device passes the hardware's (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 and v_cvt_f32_fp8 /
+// v_cvt_f32_bf8: the OCP formats, ties to even, subnormals kept; past the last midpoint NaN for E4M3, infinity for
+// E5M2). Sound for scales where fast_ok_f8 holds.
+//
+// y is within 2^-23 |y| (relative) of x / s, so x / s lies between y (1 - 2^-21) and y (1 + 2^-21), each rounded to
+// f32; rounding is monotonic, so the answer lies between their codes lo and hi. Where lo and hi agree, that is the
+// answer. Otherwise they are neighbours (the margin is far below the grid's spacing) and the midpoint between them
+// decides, as in near_f8: |x| - mid * s by one fused multiply-add has the sign of |x / s| - mid and is zero only at
+// a tie, which goes to the even code.
+//
+// Returns false, with o unspecified, where an element's |y| is not below LIMIT, the midpoint above the largest
+// finite value (464 for E4M3, 61440 for E5M2), or where hi passes the largest value: up to LIMIT nearest-even gives
+// the largest value, as the reference's saturation does, but past it (and for a NaN) the conversion's codes are not
+// the reference's. The caller then decides the chunk element by element.
+template<class T, class Word, class Decode>
+CR_HD inline bool convert_f8(const float (&x)[8], const float (&y)[8], float s, std::uint32_t (&o)[2], Word&& word,
+                             Decode&& decode) {
+  constexpr float DOWN = 0x1.fffff0p-1f, UP = 0x1.000008p+0f;           // 1 - 2^-21, 1 + 2^-21
+  constexpr std::uint32_t LIMIT = T::infinite ? 0x47700000u : 0x43e80000u;  // 61440, 464 as f32
+  std::uint32_t top = 0;  // the largest |y| pattern: a NaN's orders above every finite value and infinity
+  for(int e = 0; e < 8; ++e) {
+    const std::uint32_t u = __builtin_bit_cast(std::uint32_t, y[e]) & 0x7fffffffu;
+    top = u > top ? u : top;
+  }
+  if(top >= LIMIT) return false;
+  bool ok = true;
+  for(int h = 0; h < 2; ++h) {
+    const float* v = y + 4 * h;
+    const std::uint32_t c = word(v[0], v[1], v[2], v[3]);
+    const std::uint32_t lo = word(v[0] * DOWN, v[1] * DOWN, v[2] * DOWN, v[3] * DOWN);
+    const std::uint32_t hi = word(v[0] * UP, v[1] * UP, v[2] * UP, v[3] * UP);
+    o[h] = c;
+    if(lo == hi) continue;  // then c, between them, equals both
+    std::uint32_t out = 0;
+    for(int e = 0; e < 4; ++e) {
+      const std::uint32_t cb = (c >> (8 * e)) & 0xffu, lm = (lo >> (8 * e)) & 0x7fu, hm = (hi >> (8 * e)) & 0x7fu;
+      std::uint32_t pick = lm;
+      if(lm != hm) {  // y (1 - 2^-21) has the smaller magnitude, whatever the sign
+        ok = ok && hm <= std::uint32_t(T::largest);
+        const float mid = 0.5f * (decode(lm) + decode(hm));
+        const float d = __builtin_fmaf(-mid, s, __builtin_fabsf(x[4 * h + e]));
+        pick = d > 0.0f || (d == 0.0f && (lm & 1u)) ? hm : lm;
+      }
+      out |= ((cb & 0x80u) | pick) << (8 * e);
+    }
+    o[h] = out;
+  }
+  return ok;
+}
+
 template<class T> CR_HD inline std::uint32_t fast_f8(float x, float s, float r) {
   std::uint32_t v;
   const float y = x * r;

@@ -7,7 +7,11 @@
 // ends of the shortcut's range, and special values. Every answer must equal the oracle's, and the shortcut must
 // have both decided and declined on each boundary family (or the boundaries were never reached).
 //
-// Output: one line "checked N decided D declined E" and exit 0, or the first mismatch and exit 1.
+// The 8-bit floats' device path (convert_f8) runs here too, on an emulation of the hardware's conversion; it must
+// both decide and pass elements on.
+//
+// Output: one line "checked N decided D declined E converted C passed_on P" and exit 0, or the first mismatch and
+// exit 1.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -25,7 +29,7 @@ double oracle_decode(int f, uint32_t bits);
 namespace {
 
 using namespace cairn::quant;
-long checked = 0, decided = 0, declined = 0;
+long checked = 0, decided = 0, declined = 0, converted = 0, passed_on = 0;
 
 float bits_f(std::uint32_t u) { return __builtin_bit_cast(float, u); }
 std::uint32_t f_bits(float x) { return __builtin_bit_cast(std::uint32_t, x); }
@@ -60,6 +64,20 @@ void check_i8(float x, float s) {
   ++checked;
 }
 
+// The hardware's f32 -> 8-bit float conversion as the device kernel uses it (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 on
+// gfx950, observed on the GPU): OCP formats, round to nearest even with subnormals, no saturation. Below the midpoint
+// past the largest value that is the reference's rounding of y itself (scale 1, where saturation and rounding
+// agree); at or past it NaN (E4M3) or infinity (E5M2), NaN for a NaN. Its inverse (v_cvt_f32_fp8 / v_cvt_f32_bf8) is
+// exact: the oracle's decode.
+std::uint32_t conversion(int fmt, float y) {
+  const std::uint32_t u = f_bits(y), sign = u >> 31 << 7;
+  const std::uint32_t limit = fmt == 3 ? 0x43e80000u : 0x47700000u;  // 464, 61440
+  if((u & 0x7fffffffu) > 0x7f800000u) return sign | (fmt == 3 ? 0x7fu : 0x7eu);
+  if((u & 0x7fffffffu) >= limit) return sign | (fmt == 3 ? 0x7fu : 0x7cu);
+  int t = 0;
+  return oracle_quantize_float(fmt, y, 1.0f, &t);
+}
+
 template<class T> void check_f8(int fmt, float x, float s) {
   if(!scale_ok(s)) return;
   int t = 0;
@@ -77,6 +95,25 @@ template<class T> void check_f8(int fmt, float x, float s) {
   const std::uint32_t got = fast_ok_f8(s) ? fast_f8<T>(x, s, r) : exact_f8<T>(x, s);
   if(long(got) != want) fail(fmt == 3 ? "e4m3" : "e5m2", x, s, long(got), want);
   if(long(exact_f8<T>(x, s)) != want) fail("f8 exact", x, s, long(exact_f8<T>(x, s)), want);
+  if(fast_ok_f8(s)) {  // the device kernel's path: convert_f8 on a chunk of eight copies of the element
+    float xs[8], y[8];
+    for(int e = 0; e < 8; ++e) {
+      xs[e] = x;
+      y[e] = x * r;
+    }
+    std::uint32_t o[2] = {};
+    const auto word = [&](float a, float b, float c, float d) {
+      return conversion(fmt, a) | conversion(fmt, b) << 8 | conversion(fmt, c) << 16 | conversion(fmt, d) << 24;
+    };
+    const auto decode = [&](std::uint32_t code) { return float(oracle_decode(fmt, code)); };
+    if(convert_f8<T>(xs, y, s, o, word, decode)) {
+      ++converted;
+      if(long(o[0] & 0xffu) != want || o[0] != o[1] || (o[0] & 0xffu) * 0x01010101u != o[0])
+        fail(fmt == 3 ? "e4m3 conversion" : "e5m2 conversion", x, s, long(o[0] & 0xffu), want);
+    } else {
+      ++passed_on;
+    }
+  }
   ++checked;
 }
 
@@ -163,6 +200,11 @@ int main() {
   };
   floats(3, cr::f8e4m3{});
   floats(4, cr::f8e5m2{});
-  std::printf("checked %ld decided %ld declined %ld\n", checked, decided, declined);
+  if(converted == 0 || passed_on == 0) {
+    std::printf("the conversion path never %s\n", converted ? "passed an element on" : "decided");
+    return 1;
+  }
+  std::printf("checked %ld decided %ld declined %ld converted %ld passed_on %ld\n", checked, decided, declined,
+              converted, passed_on);
   return 0;
 }

@@ -119,6 +119,52 @@ def test_every_type_and_mode_equals_the_oracle(xname, qname):
             assert got_status == want_status, (where, got_status, want_status)
 
 
+def boundary_row(q_type: int, s: float, k: int) -> np.ndarray:
+    """x for one row at scale s: every value of the 8-bit float's grid and every midpoint between neighbours, both
+    signs, times s, and up to 3 f32 units either side of each; zeros after them to k elements."""
+    codes = np.arange(128)
+    v = np.array([H.oracle().oracle_decode(q_type, int(c)) for c in codes])
+    v = v[np.isfinite(v)]
+    grid = np.concatenate([v, (v[1:] + v[:-1]) / 2])
+    grid = np.concatenate([grid, -grid])
+    centre = (grid * s).astype(np.float32)
+    xs = [(centre.view(np.int32) + np.where(centre != 0, np.int32(d), np.int32(0))).view(np.float32) for d in range(-3, 4)]
+    x = np.concatenate(xs)
+    assert len(x) <= k
+    return np.concatenate([x, np.zeros(k - len(x), np.float32)])
+
+
+@pytest.mark.parametrize("qname", ["e4m3", "e5m2"])
+def test_the_hardware_conversion_decides_every_midpoint_as_the_oracle(qname):
+    """The fast kernel converts the 8-bit floats with the hardware's conversion and settles elements near a midpoint
+    of the grid from its neighbouring codes. Every grid value and midpoint, a few units either side, at scales whose
+    reciprocal is inexact, given per row (the kernel's wave-a-row and workgroup-a-row forms), and bf16 rows whose
+    computed scales make many quotients exact ties."""
+    q_type = Q_TYPES[qname]
+    scales = np.array([1.0, 3.0, 1 / 3, 0.37, 1.7e-6, 2.9e3, 0.1, 5.5e-3], np.float32)
+    for k in (4096, 8200):
+        x = np.stack([boundary_row(q_type, float(sc), k) for sc in scales])
+        want_q, _, want_status = H.quantize_rows(L.F32, q_type, L.SCALE_ROW, x, k, scales)
+        got_q, _, got_status = run_quantize(L.F32, q_type, L.SCALE_ROW, x, k, scales)
+        bad = np.argwhere(got_q != want_q)
+        assert bad.size == 0, (qname, k, bad[:4].tolist(), [(int(got_q[tuple(b)]), int(want_q[tuple(b)])) for b in bad[:4]])
+        assert got_status == want_status
+    # Computed scales: each row's largest magnitude a bf16 value with a short mantissa (1, 1.25, 1.5, 1.75, ...), so
+    # that x / s is often exactly a midpoint.
+    rng = np.random.default_rng(17 + q_type)
+    m, k = 64, 4096
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    tops = np.array([1.0, 1.25, 1.5, 1.75, 1.125, 1.375, 1.625, 1.875] * 8, np.float32) * np.float32(8.0)
+    x = np.clip(x, -7.0, 7.0)
+    x[np.arange(m), rng.integers(0, k, m)] = tops
+    xs = patterns(L.BF16, x)
+    want_q, want_s, _ = H.quantize_rows(L.BF16, q_type, L.SCALE_ROW_ABSMAX, xs, k)
+    got_q, got_s, _ = run_quantize(L.BF16, q_type, L.SCALE_ROW_ABSMAX, xs, k)
+    assert np.array_equal(got_s.view(np.uint32), want_s.view(np.uint32))
+    bad = np.argwhere(got_q != want_q)
+    assert bad.size == 0, (qname, bad[:4].tolist())
+
+
 def test_a_padded_output_leaves_the_padding_alone():
     rng = np.random.default_rng(11)
     x = rng.standard_normal((8, 64)).astype(np.float32)
