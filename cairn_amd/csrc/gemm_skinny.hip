@@ -423,10 +423,12 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 8192, the LDS ring
   // (4.6 against 4.4 TB/s at m = 16, and 4.0 for the streaming form, whose loads of a's 16 rows double the L2
   // traffic); otherwise the register form.
-  constexpr int ROW_WAVES = 2048;  // 8 a CU
-  const int per_wave = (p.n + ROW_WAVES - 1) / ROW_WAVES;
+  // Whole rows a wave: 8 waves a CU, 12 from n = 12288 (side by side at n = 14336, k = 4096: 5.41 TB/s against 5.30
+  // for 8 a CU, 5.35 for 4 and 5.39 for 16; below n = 12288 8 a CU was fastest at every shape tried).
+  const int row_waves = p.n >= 12288 ? 3072 : 2048;
+  const int per_wave = (p.n + row_waves - 1) / row_waves;
   if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(per_wave) * p.ldb * 2 < 0x7f000000LL) {
-    hipLaunchKernelGGL((cairn::gemm::skinny_rows<1, 8>), dim3(unsigned(ROW_WAVES / 4)), dim3(256), 0, s, p, per_wave);
+    hipLaunchKernelGGL((cairn::gemm::skinny_rows<1, 8>), dim3(unsigned(row_waves / 4)), dim3(256), 0, s, p, per_wave);
     return hipGetLastError();
   }
   if(p.m >= 2 && p.m <= 4 && p.n >= 2048) {  // rows of b a workgroup: n over the 256 CUs, 16 .. 64
