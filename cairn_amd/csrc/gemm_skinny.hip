@@ -433,7 +433,10 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   }
   if(p.m >= 2 && p.m <= 4 && p.n >= 2048) {  // rows of b a workgroup: n over the 256 CUs, 16 .. 64
     const int even = (p.n + 255) / 256;
-    const int rows = std::min(64, std::max(16, (even + 7) / 8 * 8));
+    // 32 rows (n about 8192) leave two of a workgroup's four waves idle: 16 rows, two workgroups a CU, measured 4.26
+    // against 3.24 TB/s there (m = 4, n = 8192); at the other widths tried (4096 .. 14336) this rule was best or even.
+    const int fit = std::min(64, std::max(16, (even + 7) / 8 * 8));
+    const int rows = fit == 32 ? 16 : fit;
     hipLaunchKernelGGL((cairn::gemm::skinny_stream<8>), dim3(unsigned((p.n + rows - 1) / rows)), dim3(256), 0, s, p,
                        rows);
     return hipGetLastError();
