@@ -252,14 +252,39 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   for(int i = 0; i < FM; ++i) ta_off[i] = AK ? 0 : mnmajor_fragment<ES, Sh::BM>(wr + 32 * i, 0, 0, lane);
 #pragma unroll
   for(int j = 0; j < FN; ++j) tb_off[j] = BKM ? 0 : mnmajor_fragment<ES, Sh::BN>(wc + 32 * j, 0, 0, lane);
+  // The same offsets two stages on. Ring slots 2 and 3 start 64 KiB or more into the ring, past the 16-bit offset
+  // field of an LDS read; from these bases their reads keep an immediate offset, with no address add in the loop.
+  // Opaque to the compiler, which would otherwise fold them back into the offsets above plus a constant too large.
+  int ta_hi[FM], tb_hi[FN];
+#pragma unroll
+  for(int i = 0; i < FM; ++i) {
+    ta_hi[i] = ta_off[i] + 2 * Sh::STAGE;
+    asm volatile("" : "+v"(ta_hi[i]));
+  }
+#pragma unroll
+  for(int j = 0; j < FN; ++j) {
+    tb_hi[j] = tb_off[j] + 2 * Sh::STAGE;
+    asm volatile("" : "+v"(tb_hi[j]));
+  }
 
-  // Read X of a k-step's READS: a's fragments first (one b128 each, or two transpose halves), then b's.
-  auto read = [&](auto buf, const char* stage, auto s, auto x) {
+  // A stage's place in the ring: `slot` is its index there, a constant in the unrolled steady loop (so that every LDS
+  // address and M0 value is an immediate) or an int.
+  auto stage_at = [&](auto slot) { return lds + int(slot) * Sh::STAGE; };
+  // Read X of a k-step's READS from ring slot `slot` (a constant in the unrolled steady loop, else an int): a's
+  // fragments first (one b128 each, or two transpose halves), then b's.
+  auto read = [&](auto buf, auto slot, auto s, auto x) {
     constexpr int X = decltype(x)::value, BUF = decltype(buf)::value, KS = decltype(s)::value;
+    const char* stage = stage_at(slot);
+    // The first byte of a transpose read's block i at k-step 0, half 0, from lo (slot's offsets) or hi.
+    auto block = [&](const auto& lo, const auto& hi, int i) -> const char* {
+      if constexpr(std::is_integral_v<decltype(slot)>) return stage + lo[i];
+      else if constexpr(decltype(slot)::value >= 2) return lds + hi[i] + (decltype(slot)::value - 2) * Sh::STAGE;
+      else return stage + lo[i];
+    };
     if constexpr(X < RA) {
       if constexpr(AK) xa[BUF][X] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(wr + 32 * X, KS, lane));
       else {
-        const u32x2 h = transpose_half<ES>(stage + ta_off[X / 2] + mnmajor_step<ES, Sh::BM>(KS, X % 2));
+        const u32x2 h = transpose_half<ES>(block(ta_off, ta_hi, X / 2) + mnmajor_step<ES, Sh::BM>(KS, X % 2));
         xa[BUF][X / 2][2 * (X % 2)] = h[0];
         xa[BUF][X / 2][2 * (X % 2) + 1] = h[1];
       }
@@ -268,7 +293,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
       const char* bs = stage + Sh::A_BYTES;
       if constexpr(BKM) xb[BUF][Y] = *reinterpret_cast<const u32x4*>(bs + kmajor_fragment(wc + 32 * Y, KS, lane));
       else {
-        const u32x2 h = transpose_half<ES>(bs + tb_off[Y / 2] + mnmajor_step<ES, Sh::BN>(KS, Y % 2));
+        const u32x2 h = transpose_half<ES>(block(tb_off, tb_hi, Y / 2) + Sh::A_BYTES + mnmajor_step<ES, Sh::BN>(KS, Y % 2));
         xb[BUF][Y / 2][2 * (Y % 2)] = h[0];
         xb[BUF][Y / 2][2 * (Y % 2) + 1] = h[1];
       }
@@ -278,9 +303,6 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
     constexpr int X = decltype(x)::value, BUF = decltype(buf)::value, I = X / FN, J = X % FN;
     acc[I][J] = M::step(xb[BUF][J], xa[BUF][I], acc[I][J]);
   };
-  // A stage's place in the ring: `slot` is its index there, a constant in the unrolled steady loop (so that every LDS
-  // address and M0 value is an immediate) or an int.
-  auto stage_at = [&](auto slot) { return lds + int(slot) * Sh::STAGE; };
   using LA = Loader<Sh, Sh::BM, AK, Dma>;
   using LB = Loader<Sh, Sh::BN, BKM, Dma>;
   // One operand's part of stage st (ring slot `slot`): M0 once, then its loads by immediate offset; with `tail`, each
@@ -321,7 +343,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   using K1 = std::integral_constant<int, 1>;
   wait_loads<(S - 2) * LOADS + Sh::LOADS_A>();
   fenced_barrier();
-  unrolled<READS>([&](auto x) { read(B0{}, stage_at(K0{}), K0{}, x); });
+  unrolled<READS>([&](auto x) { read(B0{}, K0{}, K0{}, x); });
 
   // The loop's buffer resources, walked a stage at a time: b's from stage S - 1 (iteration 0 loads its b), a's from
   // stage S. Each is computed after MFMAs 8 (its bytes) and 9 (the resource) of the k-step before the one that loads
@@ -349,15 +371,13 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
       if constexpr(std::is_integral_v<decltype(slot)>) return (slot + S - 1) % S;
       else return std::integral_constant<int, (decltype(slot)::value + S - 1) % S>{};
     }();
-    const char* cur = stage_at(slot);
-    const char* nxt = stage_at(next);
     const int sb = it + S - 1, sa = it + S;  // the stages whose b's, then a's, loads this iteration issues
     unrolled<16>([&](auto x) {
       constexpr int X = decltype(x)::value;
       mfma(B0{}, x);
       fence();
-      if constexpr(2 * X < READS) read(B1{}, cur, K1{}, std::integral_constant<int, 2 * X>{});
-      if constexpr(2 * X + 1 < READS) read(B1{}, cur, K1{}, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(2 * X < READS) read(B1{}, slot, K1{}, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(B1{}, slot, K1{}, std::integral_constant<int, 2 * X + 1>{});
       if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_B) load_b(rb, sb, slot_b, std::integral_constant<int, X / 4>{}, tail);
       if constexpr(X == 8) records = wa.records();
       if constexpr(X == 9) ra = Dma::resource(wa.at, records);
@@ -374,8 +394,8 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
       constexpr int X = decltype(x)::value;
       mfma(B1{}, x);
       fence();
-      if constexpr(2 * X < READS) read(B0{}, nxt, K0{}, std::integral_constant<int, 2 * X>{});
-      if constexpr(2 * X + 1 < READS) read(B0{}, nxt, K0{}, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(2 * X < READS) read(B0{}, next, K0{}, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(B0{}, next, K0{}, std::integral_constant<int, 2 * X + 1>{});
       if constexpr(X % 4 == 2 && X / 4 < Sh::LOADS_A) load_a(ra, sa, slot, std::integral_constant<int, X / 4>{}, tail);
       if constexpr(X == 8) records = wb.records();
       if constexpr(X == 9) rb = Dma::resource(wb.at, records);
@@ -481,13 +501,30 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   for(int i = 0; i < FM; ++i) ta_off[i] = AK ? 0 : mnmajor_fragment<ES, Sh::BM>(wr + 32 * i, 0, 0, lane);
 #pragma unroll
   for(int j = 0; j < FN; ++j) tb_off[j] = BKM ? 0 : mnmajor_fragment<ES, Sh::BN>(wc + 32 * j, 0, 0, lane);
-  // Read X of a stage's READS: k-step X / STEP_READS, then as wave_gemm orders a k-step's reads.
-  auto read = [&](auto buf, const char* stage, auto x) {
+  int ta_hi[FM], tb_hi[FN];  // the same two stages on, opaque: ring slots 2 and 3 (as in wave_gemm)
+#pragma unroll
+  for(int i = 0; i < FM; ++i) {
+    ta_hi[i] = ta_off[i] + 2 * Sh::STAGE;
+    asm volatile("" : "+v"(ta_hi[i]));
+  }
+#pragma unroll
+  for(int j = 0; j < FN; ++j) {
+    tb_hi[j] = tb_off[j] + 2 * Sh::STAGE;
+    asm volatile("" : "+v"(tb_hi[j]));
+  }
+  // Read X of a stage's READS from ring slot `slot`: k-step X / STEP_READS, then as wave_gemm orders a k-step's reads.
+  auto read = [&](auto buf, auto slot, auto x) {
     constexpr int BUF = decltype(buf)::value, X = decltype(x)::value % STEP_READS, s = decltype(x)::value / STEP_READS;
+    const char* stage = stage_at(slot);
+    auto block = [&](const auto& lo, const auto& hi, int i) -> const char* {
+      if constexpr(std::is_integral_v<decltype(slot)>) return stage + lo[i];
+      else if constexpr(decltype(slot)::value >= 2) return lds + hi[i] + (decltype(slot)::value - 2) * Sh::STAGE;
+      else return stage + lo[i];
+    };
     if constexpr(X < RA) {
       if constexpr(AK) xa[BUF][s][X] = *reinterpret_cast<const u32x4*>(stage + kmajor_fragment(wr + 32 * X, s, lane));
       else {
-        const u32x2 h = transpose_half<ES>(stage + ta_off[X / 2] + mnmajor_step<ES, Sh::BM>(s, X % 2));
+        const u32x2 h = transpose_half<ES>(block(ta_off, ta_hi, X / 2) + mnmajor_step<ES, Sh::BM>(s, X % 2));
         xa[BUF][s][X / 2][2 * (X % 2)] = h[0];
         xa[BUF][s][X / 2][2 * (X % 2) + 1] = h[1];
       }
@@ -496,7 +533,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
       const char* bs = stage + Sh::A_BYTES;
       if constexpr(BKM) xb[BUF][s][Y] = *reinterpret_cast<const u32x4*>(bs + kmajor_fragment(wc + 32 * Y, s, lane));
       else {
-        const u32x2 h = transpose_half<ES>(bs + tb_off[Y / 2] + mnmajor_step<ES, Sh::BN>(s, Y % 2));
+        const u32x2 h = transpose_half<ES>(block(tb_off, tb_hi, Y / 2) + Sh::A_BYTES + mnmajor_step<ES, Sh::BN>(s, Y % 2));
         xb[BUF][s][Y / 2][2 * (Y % 2)] = h[0];
         xb[BUF][s][Y / 2][2 * (Y % 2) + 1] = h[1];
       }
@@ -510,7 +547,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   for(int st = 0; st < S; ++st) stage_all(st);
   wait_loads<(S - 1) * LOADS>();
   fenced_barrier();
-  unrolled<READS>([&](auto x) { read(std::integral_constant<int, 0>{}, stage_at(std::integral_constant<int, 0>{}), x); });
+  unrolled<READS>([&](auto x) { read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, x); });
 
   // Iteration `it` loads stage it + S into the slot stage it leaves. Its resources are walked a stage at a time and
   // made after MFMAs 12 .. 15 of the iteration before, slots no load uses; steady iterations (stages that end
@@ -530,7 +567,6 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
       else return std::integral_constant<int, (decltype(slot)::value + 1) % S>{};
     }();
     const int sl = it + S;  // the stage whose loads this iteration issues, into stage it's slot
-    const char* nxt = stage_at(next);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wait_loads<(S - 2) * LOADS>();
     fenced_barrier();
@@ -538,8 +574,8 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
       constexpr int X = decltype(x)::value;
       mfma(std::integral_constant<int, C>{}, x);
       fence();
-      if constexpr(2 * X < READS) read(std::integral_constant<int, N>{}, nxt, std::integral_constant<int, 2 * X>{});
-      if constexpr(2 * X + 1 < READS) read(std::integral_constant<int, N>{}, nxt, std::integral_constant<int, 2 * X + 1>{});
+      if constexpr(2 * X < READS) read(std::integral_constant<int, N>{}, next, std::integral_constant<int, 2 * X>{});
+      if constexpr(2 * X + 1 < READS) read(std::integral_constant<int, N>{}, next, std::integral_constant<int, 2 * X + 1>{});
       if constexpr(X >= 4 && X < 4 + Sh::LOADS_A) load_a(ra, sl, slot, std::integral_constant<int, X - 4>{}, tail);
       if constexpr(X >= 8 && X < 8 + Sh::LOADS_B) load_b(rb, sl, slot, std::integral_constant<int, X - 8>{}, tail);
       if constexpr(X == 12) records = wa.records();
