@@ -47,20 +47,24 @@ __device__ __forceinline__ void col_terms(const Params& p, int n0, int lane, flo
 // The epilogue's steps on one accumulator value, each an f32 rounding, in the order cairn_gemm.h states. ACT is a
 // template argument: callers branch on p.act once, outside their loops, so that a loop holds only its own
 // activation's code (256 unrolled copies of GELU that a plain store jumps over still crowd the instruction cache).
+// ACT_SCALES: no activation and no bias (the W8A8 dequant), so the bias step, an add of -0 that changes no value,
+// is left out.
+constexpr int ACT_SCALES = -1;
 template<int ACT>
 __device__ __forceinline__ float apply(float v, float rs, float cs, float bs) {
   v = v * rs;
   v = v * cs;
-  v = v + bs;
+  if constexpr(ACT != ACT_SCALES) v = v + bs;
   if constexpr(ACT == CAIRN_ACT_RELU) v = v < 0.0f ? 0.0f : v;
   else if constexpr(ACT == CAIRN_ACT_GELU) v = gelu(v);
   return v;
 }
 
-// f(integral_constant<ACT>) for the activation p.act names.
+// f(integral_constant<ACT>) for the activation p.act names, ACT_SCALES where there is neither activation nor bias.
 template<class F> __device__ __forceinline__ void with_act(const Params& p, F&& f) {
   if(p.act == CAIRN_ACT_GELU) f(std::integral_constant<int, CAIRN_ACT_GELU>{});
   else if(p.act == CAIRN_ACT_RELU) f(std::integral_constant<int, CAIRN_ACT_RELU>{});
+  else if(!p.bias) f(std::integral_constant<int, ACT_SCALES>{});
   else f(std::integral_constant<int, CAIRN_ACT_NONE>{});
 }
 
