@@ -397,7 +397,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--only", choices=["square", "skinny", "mlp", "quantize", "all", "traffic", "calibrate"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--family", choices=["pipe", "wave"], help="run the square GEMMs on this kernel family")
+    ap.add_argument("--family", choices=["wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
     args = ap.parse_args()
     if args.summarize:

@@ -15,6 +15,8 @@ import shutil
 import subprocess
 from pathlib import Path
 
+from cairn_amd import identity
+
 HERE = Path(__file__).resolve().parent
 SOURCES = HERE / "csrc"
 OBJECTS = HERE / "_build"
@@ -46,6 +48,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every source and link the library; returns its path. Always rebuilds."""
     if not shutil.which(HIPCC) and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
+    identity.check()  # the header's interface identity is the hash of what it states
     OBJECTS.mkdir(exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 16)

@@ -14,9 +14,6 @@ using Launcher = hipError_t (*)(const Params&, hipStream_t);
 #define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
 #include "instances.inc"
 #undef CAIRN_MFMA_INSTANCE
-#define CAIRN_PIPE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
-#include "pipe_instances.inc"
-#undef CAIRN_PIPE_INSTANCE
 #define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
 #define CAIRN_WAVE8_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) hipError_t NAME(const Params&, hipStream_t);
 #include "wave_instances.inc"
@@ -31,7 +28,7 @@ namespace {
 constexpr int CUS = 256;              // gfx950: 8 XCDs of 32 CUs (MI350X, MI355X)
 constexpr int LDS_PER_CU = 160 * 1024;
 
-enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2, PIPE = 3, WAVE = 4 };
+enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2, WAVE = 4 };  // 3 was an eight-wave kernel, retired
 
 struct Kernel {
   Launcher run;
@@ -44,18 +41,15 @@ struct Kernel {
 };
 
 #define CAIRN_MFMA_INSTANCE(NAME, BM, BN, OP, TA, TB) {NAME, MFMA, OP, TA, TB, BM, BN, #NAME, 2},
-#define CAIRN_PIPE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, PIPE, OP, TA, TB, BM, BN, #NAME, STAGES},
 #define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, WAVE, OP, TA, TB, BM, BN, #NAME, STAGES},
 #define CAIRN_WAVE8_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB) {NAME, WAVE, OP, TA, TB, BM, BN, #NAME, STAGES},
 const Kernel TABLE[] = {
     {nullptr, GENERIC, -1, false, false, 64, 64, "cairn_generic_64x64", 1},
     {nullptr, SKINNY, cairn::gemm::OP_BF16, false, true, 16, 64, "cairn_skinny_bf16_nt", 0},
 #include "instances.inc"
-#include "pipe_instances.inc"
 #include "wave_instances.inc"
 };
 #undef CAIRN_MFMA_INSTANCE
-#undef CAIRN_PIPE_INSTANCE
 #undef CAIRN_WAVE_INSTANCE
 #undef CAIRN_WAVE8_INSTANCE
 constexpr int COUNT = int(sizeof(TABLE) / sizeof(TABLE[0]));
@@ -97,8 +91,10 @@ int check(const cairn_gemm_desc* in, Problem& out) {
   if(d.act < CAIRN_ACT_NONE || d.act > CAIRN_ACT_GELU) return CAIRN_E_ARG;
   if(d.bias && d.bias_type != CAIRN_TYPE_F32 && d.bias_type != CAIRN_TYPE_BF16) return CAIRN_E_TYPE;
   if((d.trans_a != 0 && d.trans_a != 1) || (d.trans_b != 0 && d.trans_b != 1)) return CAIRN_E_ARG;
-  constexpr std::uint64_t LIMIT = 0x7fffffffULL;
-  if(d.m > LIMIT || d.n > LIMIT || d.k > LIMIT) return CAIRN_E_SHAPE;
+  // Extents leave room below 2^31 for the largest tile: the kernels compare row0 + BM (col0 + BN, k0 + BK) with an
+  // extent in 32-bit arithmetic, which must not wrap for the last tile.
+  constexpr std::uint64_t LIMIT = 0x7fffffffULL, EXTENT = 0x7fffff00ULL;
+  if(d.m > EXTENT || d.n > EXTENT || d.k > EXTENT) return CAIRN_E_SHAPE;
   const std::uint64_t arow = d.trans_a ? d.m : d.k, brow = d.trans_b ? d.k : d.n;
   if(!d.lda) d.lda = arow;
   if(!d.ldb) d.ldb = brow;
@@ -133,10 +129,10 @@ bool mfma_fits(const cairn_gemm_desc& d, const Kernel& k) {
   return a_ok && b_ok && c_ok;
 }
 
-// Can a kernel of the LDS ring (pipelined, or one wave a SIMD) take it: 16-byte loads whole and aligned (K-major rows
+// Can a kernel of the LDS ring (one wave a SIMD) take it: 16-byte loads whole and aligned (K-major rows
 // in chunks of 16 bytes of k; M/N-major rows in chunks of 16 bytes of columns), offsets inside int32.
-bool ring(const Kernel& k) { return k.family == PIPE || k.family == WAVE; }
-bool pipe_fits(const cairn_gemm_desc& d, const Kernel& k) {
+bool ring(const Kernel& k) { return k.family == WAVE; }
+bool ring_fits(const cairn_gemm_desc& d, const Kernel& k) {
   if(!ring(k) || k.op != op_of(d.ab_type) || k.ta != bool(d.trans_a) || k.tb != bool(d.trans_b)) return false;
   const int es = element_size(d.ab_type), ce = 16 / es;
   const std::uint64_t bk = 64 / es;
@@ -153,11 +149,11 @@ bool pipe_fits(const cairn_gemm_desc& d, const Kernel& k) {
   // The one-wave-a-SIMD kernel loads by immediate offsets (pipe.hpp, Loader::imm_fits): a K-major operand's rows at
   // least a stage's 64 bytes apart, an M/N-major operand's k rows at least a tile's width of elements apart.
   auto imm = [&](bool kmaj, std::uint64_t ld, int width) { return kmaj ? ld * es >= 64 : ld >= std::uint64_t(width); };
-  const bool imm_ok = k.family != WAVE || (imm(!d.trans_a, d.lda, k.bm) && imm(bool(d.trans_b), d.ldb, k.bn));
+  const bool imm_ok = (imm(!d.trans_a, d.lda, k.bm) && imm(bool(d.trans_b), d.ldb, k.bn));
   return a_ok && b_ok && c_ok && imm_ok;
 }
 
-bool tiled_fits(const cairn_gemm_desc& d, const Kernel& k) { return ring(k) ? pipe_fits(d, k) : mfma_fits(d, k); }
+bool tiled_fits(const cairn_gemm_desc& d, const Kernel& k) { return ring(k) ? ring_fits(d, k) : mfma_fits(d, k); }
 
 // The skinny kernel: bf16, b stored n x k (the decode layout), m <= 16, every row 16-byte whole.
 bool skinny_fits(const cairn_gemm_desc& d) {
@@ -182,7 +178,6 @@ int resident(const Kernel& k) {
 // MFMA from LDS and L2. These are the selector's model, refit from the measured rates the benchmark records.
 double shape_rate(const Kernel& k) {
   const int area = k.bm * k.bn;
-  if(k.family == PIPE) return area >= 256 * 256 ? 2.0 : (area >= 256 * 128 ? 1.8 : 1.5);
   if(k.family == WAVE) return area >= 256 * 256 ? 2.2 : (area >= 256 * 128 ? 1.9 : 1.6);
   if(area >= 256 * 256) return 1.0;
   if(area >= 256 * 128) return 0.92;
@@ -277,6 +272,7 @@ Params params_of(const cairn_gemm_desc& d, const Kernel& k) {
   p.bias_type = d.bias_type;
   p.row_scale = d.row_scale;
   p.col_scale = d.col_scale;
+  p.rows16 = aligned(d.c, 16) && (d.ldc * std::uint64_t(output_size(d.c_type))) % 16 == 0;
   return p;
 }
 
@@ -284,7 +280,8 @@ Params params_of(const cairn_gemm_desc& d, const Kernel& k) {
 
 extern "C" {
 
-const char cairn_interface_gemm_gfx950_1[] = "cairn_gemm_gfx950";
+// The interface identity the header derives from its stated interface (CAIRN_GEMM_IDENTITY), naming the library.
+__attribute__((visibility("default"))) const char CAIRN_GEMM_IDENTITY[] = "gemm_gfx950";
 
 int cairn_gemm_kernel_count(void) { return COUNT; }
 
@@ -304,7 +301,7 @@ int cairn_gemm_kernel_info(int32_t id, cairn_gemm_kernel* out) {
   out->tile_m = k.bm;
   out->tile_n = k.bn;
   out->tile_k = tile_k(k);
-  out->threads = k.family == PIPE ? 512 : 256;
+  out->threads = 256;
   out->lds_bytes = lds_bytes(k);
   out->family = k.family;
   std::strncpy(out->name, k.name, sizeof(out->name) - 1);

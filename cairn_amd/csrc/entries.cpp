@@ -5,6 +5,7 @@
 // against the C++20 surface (include/cairn/), as emitted code is.
 #include <cstddef>
 #include "../../include/cairn/cairn_hip.hpp"
+#include "../../include/cairn/cairn_here.hpp"
 #include "../../include/cairn/cairn_tensor.hpp"
 
 namespace {

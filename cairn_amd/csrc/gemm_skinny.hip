@@ -140,7 +140,7 @@ __global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
 // that up to S - 1 stages (3 x 40 KiB a CU) are in flight without a register held for them, each load 2 rows x 512
 // contiguous bytes. Wave w multiplies rows 16 w .. 16 w + 15 of b (the workgroup's columns) over the whole stage, so
 // its accumulator is whole at the end and nothing is reduced across waves. One barrier a stage, as the GEMM ring
-// (gemm_wave.hip): past it the stage has landed for every wave and the stage before it is free for the refill.
+// (wave.hpp): past it the stage has landed for every wave and the stage before it is free for the refill.
 // A row's 16-byte units are stored swizzled, unit u of row r at u ^ (r % 32), so the 16 rows an MFMA operand read
 // takes are on distinct banks; the swizzle is applied by choosing which global unit each lane fetches.
 // f(integral_constant<U>) for U = 0 .. N-1.

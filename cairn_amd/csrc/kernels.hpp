@@ -30,6 +30,7 @@ struct Params {
   int bias_type;         // CAIRN_TYPE_F32 or CAIRN_TYPE_BF16
   const float* row_scale;
   const float* col_scale;
+  int rows16;            // every row of c starts on 16 bytes (c 16-byte aligned, ldc a multiple of 16 bytes)
 };
 
 __device__ inline std::uint32_t as_bits(float x) { return __builtin_bit_cast(std::uint32_t, x); }

@@ -1,7 +1,7 @@
-// The index arithmetic of the pipelined gfx950 GEMM (gemm_pipe.hip), written once for the kernel and for the host
-// simulator (tests/sim/tile_sim.cpp).
+// The index arithmetic of the LDS-ring gfx950 GEMM (wave.hpp), written once for the kernel and for the host simulator
+// (tests/sim/tile_sim.cpp). The simulator also runs it for eight waves a workgroup, the form of an earlier kernel.
 //
-// A workgroup of eight waves computes a BM x BN tile. Operand tiles cross from global memory straight into LDS
+// A workgroup computes a BM x BN tile. Operand tiles cross from global memory straight into LDS
 // (buffer_load_dwordx4 ... lds: lane l of a wave's load writes 16 bytes at the wave's LDS base + 16 l), STAGES deep,
 // 64 bytes of every row's k per stage (32 bf16/f16 or 64 int8: two MFMA k-steps). Each operand keeps the layout it
 // has in memory:
@@ -28,8 +28,8 @@
 namespace cairn::pipe {
 using cairn::tile::u32x4;
 
-// WAVES 8: two groups of four waves (gemm_pipe.hip), a wave holding (BM/2) x (BN/4) outputs; WAVES 4: one wave a
-// SIMD (gemm_wave.hip), a wave holding (BM/2) x (BN/2). Either way a stage's loads are spread over 256 threads: one
+// WAVES 8: two groups of four waves (the earlier ping-pong form, simulated only), a wave holding (BM/2) x (BN/4)
+// outputs; WAVES 4: one wave a SIMD (wave.hpp), a wave holding (BM/2) x (BN/2). Either way a stage's loads are spread over 256 threads: one
 // group's for one operand (8 waves), or all four waves' for both (4 waves).
 template<int BM_, int BN_, int ES_, int STAGES_, int WAVES_ = 8> struct Shape {
   static constexpr int BM = BM_, BN = BN_, ES = ES_, STAGES = STAGES_, WAVES = WAVES_;

@@ -1,4 +1,4 @@
-// Device helpers shared by the LDS-ring GEMMs (gemm_pipe.hip, gemm_wave.hip): the buffer resource and the 16-byte
+// Device helpers of the LDS-ring GEMMs (wave.hpp) and the skinny ring (gemm_skinny.hip): the buffer resource and the 16-byte
 // global-to-LDS load that fills the ring, the waits and barrier that order it, and the MFMA operand reads.
 #pragma once
 #include <hip/hip_runtime.h>

@@ -3,9 +3,9 @@
 //
 // A workgroup of 256 threads computes one BM x BN output tile (256 x 256 by default); wave w holds the (BM/2) x
 // (BN/2) block at wave_origin (pipe.hpp), 4 x 4 blocks of 32 x 32 accumulators at 256 x 256, which live in the
-// accumulation registers. The operand stages are the ones the eight-wave kernel (gemm_pipe.hip) uses: 64 bytes of k of
-// every operand row a stage, STAGES deep, filled by buffer_load ... lds, with the same swizzles and fragment reads;
-// here all four waves load both operands, a quarter each.
+// accumulation registers. The operand stages are pipe.hpp's: 64 bytes of k of every operand row a stage, STAGES deep,
+// filled by buffer_load ... lds, with its swizzles and fragment reads; all four waves load both operands, a quarter
+// each.
 //
 // Compared with eight waves of (BM/2) x (BN/4), a wave's larger block reads a third less from LDS for the same MFMA
 // work (a stage is read 2 + 2 times, not 4 + 2), and the workgroup meets at one barrier a stage instead of two.
@@ -34,6 +34,10 @@
 // MFMA's 32 cycles take (tests/test_isa.py prices the compiled loop).
 // Scheduling fences keep the interleave as written and keep everything on its side of the barrier.
 // No atomics: the result's bits do not depend on timing.
+//
+// The instances (gemm_wave_<type>.hip, one file an operand type so they compile in parallel) are listed in
+// wave_<type>.inc; capi.cpp's kernel table reads the same lists through wave_instances.inc.
+#pragma once
 #include <hip/hip_runtime.h>
 #include <utility>
 #include "epilogue.hpp"
@@ -81,7 +85,7 @@ template<class Sh>
 __device__ __forceinline__ Terms prefetch_terms(const Params& p, int row0, int col0, int t) {
   static_assert(Sh::BM == 256 && Sh::BN == 256, "a thread a row and a column of the tile");
   Terms v;
-  const bool staged = p.c_type == CAIRN_TYPE_BF16 && row0 + Sh::BM <= p.m && col0 + Sh::BN <= p.n;
+  const bool staged = p.c_type == CAIRN_TYPE_BF16 && p.rows16 && row0 + Sh::BM <= p.m && col0 + Sh::BN <= p.n;
   if(!staged) return v;  // uniform; the other stores read their terms themselves
   if(p.row_scale) v.rs = p.row_scale[row0 + t];
   if(p.col_scale) v.cs = p.col_scale[col0 + t];
@@ -99,7 +103,7 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
   const bool plain = !p.row_scale && !p.col_scale && !p.bias && p.act == CAIRN_ACT_NONE;
   const bool whole = row0 + Sh::BM <= p.m && col0 + Sh::BN <= p.n;
   if constexpr(!RAW) {
-    if(p.c_type == CAIRN_TYPE_BF16 && whole) {
+    if(p.c_type == CAIRN_TYPE_BF16 && whole && p.rows16) {  // rows of c on 16 bytes: the staged 16-byte stores
       // The wave's WTM x WTN bf16 block goes into its own part of the ring (free once every wave has passed the
       // barrier), 8 bytes a quad, then comes back 16 bytes a lane, a row of the block per 16 lanes. The 8-byte unit u
       // of row r sits at unit u ^ (r % 32) of the row, which keeps both the writes (32 rows, one unit each) and the
@@ -623,6 +627,7 @@ template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave(const Params
 
 }  // namespace cairn::gemm
 
+// An instance of the kernel table: a launcher named NAME for one shape, operation and layout.
 #define CAIRN_WAVE_INSTANCE(NAME, BM, BN, STAGES, OP, TA, TB)                                                      \
   hipError_t NAME(const cairn::gemm::Params& p, hipStream_t s) {                                                 \
     return cairn::gemm::launch_wave<                                                                              \
@@ -632,4 +637,3 @@ template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave(const Params
   hipError_t NAME(const cairn::gemm::Params& p, hipStream_t s) {                                                 \
     return cairn::gemm::launch_wave8<cairn::pipe::Shape<BM, BN, 1, STAGES, 4>, OP, TA, TB>(p, s);                \
   }
-#include "wave_instances.inc"

@@ -14,6 +14,7 @@ from pathlib import Path
 import numpy as np
 
 _H2D, _D2H, _D2D = 1, 2, 3
+_NOT_READY = 600  # hipErrorNotReady
 _ATTR_CUS, _ATTR_CLOCK_KHZ, _ATTR_MEM_CLOCK_KHZ, _ATTR_L2 = 63, 5, 60, 19
 
 
@@ -60,6 +61,14 @@ def lib() -> C.CDLL:
             "hipDeviceGetAttribute": [C.POINTER(C.c_int), C.c_int, C.c_int],
             "hipDeviceGetName": [C.c_char_p, C.c_int, C.c_int],
             "hipGetLastError": [],
+            "hipStreamQuery": [C.c_void_p],
+            "hipStreamBeginCapture": [C.c_void_p, C.c_int],
+            "hipStreamEndCapture": [C.c_void_p, C.POINTER(C.c_void_p)],
+            "hipGraphInstantiate": [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t],
+            "hipGraphLaunch": [C.c_void_p, C.c_void_p],
+            "hipGraphExecDestroy": [C.c_void_p],
+            "hipGraphDestroy": [C.c_void_p],
+            "hipGraphGetNodes": [C.c_void_p, C.c_void_p, C.POINTER(C.c_size_t)],
         }.items():
             f = getattr(_lib, name)
             f.restype = C.c_int
@@ -164,10 +173,47 @@ class Stream:
     def synchronize(self) -> None:
         check(lib().hipStreamSynchronize(C.c_void_p(self.handle)), "hipStreamSynchronize")
 
+    def idle(self) -> bool:
+        """Whether everything queued on the stream has finished (hipStreamQuery), without waiting."""
+        status = lib().hipStreamQuery(C.c_void_p(self.handle))
+        if status == _NOT_READY:
+            return False
+        check(status, "hipStreamQuery")
+        return True
+
     def close(self) -> None:
         if self.handle:
             lib().hipStreamDestroy(C.c_void_p(self.handle))
             self.handle = None
+
+
+class Graph:
+    """What `queue(stream)` queues on `stream`, captured (hipStreamBeginCapture, global mode) into an executable
+    graph; launch() replays it on a stream."""
+
+    def __init__(self, stream: Stream, queue):
+        check(lib().hipStreamBeginCapture(C.c_void_p(stream.handle), 0), "hipStreamBeginCapture")
+        try:
+            queue(stream)
+        finally:
+            g = C.c_void_p()
+            check(lib().hipStreamEndCapture(C.c_void_p(stream.handle), C.byref(g)), "hipStreamEndCapture")
+        self.graph = g.value
+        count = C.c_size_t(0)
+        check(lib().hipGraphGetNodes(C.c_void_p(self.graph), None, C.byref(count)), "hipGraphGetNodes")
+        self.nodes = count.value
+        e = C.c_void_p()
+        check(lib().hipGraphInstantiate(C.byref(e), C.c_void_p(self.graph), None, None, 0), "hipGraphInstantiate")
+        self.exe = e.value
+
+    def launch(self, stream: Stream) -> None:
+        check(lib().hipGraphLaunch(C.c_void_p(self.exe), C.c_void_p(stream.handle)), "hipGraphLaunch")
+
+    def close(self) -> None:
+        if self.exe:
+            lib().hipGraphExecDestroy(C.c_void_p(self.exe))
+            lib().hipGraphDestroy(C.c_void_p(self.graph))
+            self.exe = self.graph = None
 
 
 class Event:

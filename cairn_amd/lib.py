@@ -9,6 +9,8 @@ from __future__ import annotations
 import ctypes as C
 from pathlib import Path
 
+from cairn_amd import identity
+
 HERE = Path(__file__).resolve().parent
 LIBRARY = HERE / "libcairn_gemm_gfx950.so"
 
@@ -21,7 +23,7 @@ DESC_VERSION = 1
 SCALE_ROW_ABSMAX, SCALE_ROW, SCALE_TENSOR = range(3)
 QUANT_BAD_SCALE, QUANT_NAN = 1, 2
 QUANTIZE_DESC_VERSION = 1
-FAMILY = {0: "mfma", 1: "generic", 2: "skinny", 3: "pipe", 4: "wave"}
+FAMILY = {0: "mfma", 1: "generic", 2: "skinny", 4: "wave"}
 TYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", F8E4M3: "f8e4m3", F8E5M2: "f8e5m2", I8: "i8", I32: "i32"}
 
 
@@ -131,7 +133,7 @@ SIGNATURES = {
     **{f"cf_mma_{f}_device": (None, _MMA) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
     **{f"cq_mma_{f}_device": (None, [C.c_void_p, *_MMA]) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
 }
-DATA_SYMBOLS = ["cairn_interface_gemm_gfx950_1"]
+DATA_SYMBOLS = [identity.declared()]  # the interface identity include/cairn_gemm.h names
 
 _lib: C.CDLL | None = None
 

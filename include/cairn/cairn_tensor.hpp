@@ -52,20 +52,20 @@ template<class A> constexpr int type_of() noexcept {
   else static_assert(sizeof(A) == 0, "mma_unordered multiplies storage floats");
 }
 
-// On the calling thread's execution context: the multiply runs on its synchronous lane and the call returns once that
+// On the calling thread's execution context: the multiply runs as its synchronous work and the call returns once that
 // stream has run it (in a held run, at the run's end; under an enqueued call, never). m or n of 0 queues nothing,
 // and so does k of 0, which leaves c as it is.
-template<class A, class Api>
-inline void launch(reuse::Context<Api>& ctx, std::size_t m, std::size_t n, std::size_t k, float* c, std::size_t cn,
+template<class A, class M>
+inline void launch(reuse::Context<M>& ctx, std::size_t m, std::size_t n, std::size_t k, float* c, std::size_t cn,
                    const A* a, std::size_t an, const A* b, std::size_t bn) noexcept {
   shape(m, n, k, cn, an, bn);
   if(!m || !n || !k) return;
-  reuse::synchronous(ctx, [&](typename Api::Stream s) { ctx.api().mma(type_of<A>(), m, n, k, c, a, b, s); });
+  reuse::synchronous(ctx, [&](typename M::Stream s) { ctx.machine().mma(type_of<A>(), m, n, k, c, a, b, s); });
 }
 
-// Any GEMM the C ABI describes, on the context's synchronous lane.
-template<class Api> inline void gemm(reuse::Context<Api>& ctx, const cairn_gemm_desc& d) noexcept {
-  reuse::synchronous(ctx, [&](typename Api::Stream s) { ctx.api().gemm(d, s); });
+// Any GEMM the C ABI describes, as synchronous work on the context.
+template<class M> inline void gemm(reuse::Context<M>& ctx, const cairn_gemm_desc& d) noexcept {
+  reuse::synchronous(ctx, [&](typename M::Stream s) { ctx.machine().gemm(d, s); });
 }
 
 }  // namespace cr::tensor

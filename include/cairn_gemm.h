@@ -32,6 +32,7 @@
 extern "C" {
 #endif
 
+/* cairn:stated-begin */
 /* Storage floats as the C header states them (header.py:276-277): the pattern and nothing else. */
 typedef struct { uint16_t bits; } cairn_f16;
 typedef struct { uint16_t bits; } cairn_bf16;
@@ -209,9 +210,22 @@ typedef struct cairn_quantize_desc {
 } cairn_quantize_desc;
 
 int cairn_quantize_run(const cairn_quantize_desc* d, void* stream);
+/* cairn:stated-end */
 
-/* The interface identity: defined by the library built with this header (header.py:280-285). */
-extern const char cairn_interface_gemm_gfx950_1[];
+/*
+ * The interface identity, derived as CAIRN's header generator derives a library's (header.py:280-285):
+ * cairn_interface_<library>_<the first 16 hex digits of the SHA-256 of the stated interface>, the text between the
+ * two cairn:stated markers above, byte for byte. The library built with this header defines the symbol, and the
+ * header refers to it, so a program built against another version of this header fails to link instead of passing
+ * descriptors whose fields have moved. cairn_amd/identity.py recomputes it (and rewrites this line with --write);
+ * the build refuses a header whose identity is stale. A translation unit that uses the header's types without the
+ * library (a host-only test machine, or an emulated build: CAIRN_EMULATE) defines CAIRN_GEMM_UNLINKED.
+ */
+#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_41cf1b6ef10665c0
+extern const char CAIRN_GEMM_IDENTITY[];
+#if !defined(CAIRN_GEMM_UNLINKED) && !defined(CAIRN_EMULATE)
+static const char* const cairn_interface_of_gemm_gfx950 __attribute__((used)) = CAIRN_GEMM_IDENTITY;
+#endif
 
 #ifdef __cplusplus
 }

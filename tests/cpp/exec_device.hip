@@ -1,5 +1,5 @@
-// The HIP execution layer (include/cairn/cairn_hip_exec.hpp over cairn_context.hpp) on the device, in programs
-// shaped as CAIRN-emitted device code is: regions on the thread's context, reductions, scans and a compaction from
+// The HIP execution layer (include/cairn/cairn_ops.hpp and cairn_hip_kernels.hpp over cairn_context.hpp) on the
+// device, in programs shaped as CAIRN-emitted device code is: regions on the thread's context, reductions, scans and a compaction from
 // its arena, the vector and staged plans, owners of device, pinned and unified storage, held runs, an enqueued call
 // on the caller's stream, queued work on lent lanes, and a context with a budget of its own. Built by
 // __graft_entry__.build() into tests/cpp/libexec_device.so; tests/test_gpu_exec.py calls it and checks every result
@@ -106,7 +106,7 @@ extern "C" int exec_queue(std::size_t n, int* out) {
   wait(std::move(second));
   wait(std::move(first));
   copy_on(ctx, out, c.data(), n, Dir::d2h);
-  return ctx.lent() == 0 ? 0 : 1;
+  return ctx.tickets() == 0 ? 0 : 1;
 }
 
 // A context with a budget of its own: stream-ordered growth to a limit, over_budget past it, ok again within it.
@@ -127,7 +127,7 @@ extern "C" int exec_budget(std::size_t limit, std::size_t big, int* answers, std
   answers[2] = int(reduce(own, r, 10, 0LL, Add{}, [] __host__ __device__(std::size_t i) { return (long long)i; }));
   caps[2] = own.capacity();
   *total = r;
-  return own.lent() == 0 ? 0 : 3;
+  return own.tickets() == 0 ? 0 : 3;
 }
 
 // Owners of pinned and unified storage, and zero() at an odd address: out[0 .. 16) the unified squares the device
@@ -153,7 +153,7 @@ extern "C" int exec_owners(int* out, unsigned char* bytes) {
   Buffer<unsigned char> z(37);
   unsigned char* pz = z.data();
   run(ctx, 37, [=] __device__(std::size_t i) { pz[i] = 0xff; });
-  cr::reuse::synchronous(ctx, [&](hipStream_t s) { ctx.api().zero(pz + 1, 35, s); });
+  cr::reuse::synchronous(ctx, [&](hipStream_t s) { ctx.machine().zero(pz + 1, 35, s); });
   copy_on(ctx, bytes, pz, 37, Dir::d2h);
   return 0;
 }

@@ -257,7 +257,7 @@ template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k,
     }
 }
 
-// ---------------------------------------------------------------- the pipelined kernel (gemm_pipe.hip, pipe.hpp)
+// ---------------------------------------------------------------- the LDS-ring kernels' index math (pipe.hpp; wave.hpp, and eight waves a workgroup)
 
 bool bad_read = false;
 bool conflict = false;

@@ -7,6 +7,7 @@ BASELINE config and refuses what no kernel computes. No test here launches GPU w
 from __future__ import annotations
 
 import ctypes as C
+import hashlib
 import re
 import subprocess
 import sys
@@ -16,6 +17,7 @@ import numpy as np
 import pytest
 
 import helpers as H
+from cairn_amd import identity
 from cairn_amd import lib as L
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -39,14 +41,55 @@ def test_the_library_exports_every_declared_symbol():
     assert not missing, missing
     assert names == set(L.SIGNATURES), names ^ set(L.SIGNATURES)  # the bindings type every entry
     lib = L.load()
-    assert C.c_char_p.in_dll(lib, "cairn_interface_gemm_gfx950_1") is not None
+    assert (C.c_char * 12).in_dll(lib, L.DATA_SYMBOLS[0]).value == b"gemm_gfx950"
+
+
+def test_the_interface_identity_is_the_hash_of_the_stated_interface():
+    """header.py:280-285: cairn_interface_<library>_<sha256 of the stated interface, 16 hex digits>. The header's line
+    is the hash of its own stated text, the library defines exactly that symbol, and a change to any declaration
+    changes it."""
+    text = HEADER.read_text()
+    stated = identity.stated(text)
+    assert "int cairn_gemm_run(" in stated and "cairn_quantize_desc" in stated
+    assert identity.declared(text) == identity.check()
+    assert identity.derived(text) == "cairn_interface_gemm_gfx950_" + hashlib.sha256(stated.encode()).hexdigest()[:16]
+    edited = text.replace("int cairn_gemm_run(const cairn_gemm_desc* d, void* stream);",
+                          "int cairn_gemm_run(const cairn_gemm_desc* d, void* stream, int flags);")  # fmt: skip
+    assert edited != text and identity.derived(edited) != identity.derived(text)
+    dynamic = subprocess.run(["nm", "-D", "--defined-only", str(L.LIBRARY)], capture_output=True, text=True,
+                             check=True).stdout  # fmt: skip
+    ids = {line.split()[-1] for line in dynamic.splitlines() if "cairn_interface_" in line}
+    assert ids == {identity.declared(text)}
+    assert (C.c_char * 12).in_dll(L.load(), identity.declared(text)).value == b"gemm_gfx950"  # a char array
+
+
+def test_a_program_built_against_another_version_of_the_header_fails_to_link(tmp_path):
+    """The header refers to its identity, so a program that includes it needs the library of the same stated
+    interface: against this header it links; against a copy whose run entry gained a parameter (and so a new
+    identity, written as identity.py writes it) the link fails on that identity's symbol."""
+    src = tmp_path / "caller.c"
+    src.write_text('#include "cairn_gemm.h"\nint main(void) { return cairn_gemm_kernel_count() > 0 ? 0 : 1; }\n')
+    def link(include: Path) -> subprocess.CompletedProcess:
+        return subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{include}", str(src), "-o",
+                               str(tmp_path / "caller"), f"-L{L.LIBRARY.parent}", f"-l:{L.LIBRARY.name}",
+                               f"-Wl,-rpath,{L.LIBRARY.parent}"], capture_output=True, text=True)  # fmt: skip
+    assert link(HEADER.parent).returncode == 0
+    stale = tmp_path / "stale"
+    stale.mkdir()
+    text = HEADER.read_text().replace("int cairn_gemm_run(const cairn_gemm_desc* d, void* stream);",
+                                      "int cairn_gemm_run(const cairn_gemm_desc* d, void* stream, int flags);")
+    other = identity.derived(text)
+    (stale / "cairn_gemm.h").write_text(identity.DEFINE.sub(f"#define CAIRN_GEMM_IDENTITY {other}", text))
+    done = link(stale)
+    assert done.returncode != 0 and other in done.stderr, done.stderr
 
 
 def test_the_structs_have_the_layout_the_header_states(tmp_path):
     structs = {"cairn_gemm_desc": L.Desc, "cairn_gemm_kernel": L.Kernel, "cairn_gemm_choice": L.Choice,
                "cairn_quantize_desc": L.QuantizeDesc}  # fmt: skip
     fields = {name: [f for f, _ in cls._fields_] for name, cls in structs.items()}
-    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", "#define CAIRN_GEMM_UNLINKED 1", f'#include "{HEADER}"',
+             "int main(void) {"]  # the layouts only: no library to link
     for struct, names in fields.items():
         lines.append(f'printf("{struct} %zu\\n", sizeof({struct}));')
         lines += [f'printf("{struct}.{f} %zu\\n", offsetof({struct}, {f}));' for f in names]
@@ -132,10 +175,10 @@ def choose(*args, **kw):
 
 def test_the_selector_picks_a_kernel_for_every_baseline_config():
     c2 = choose(L.BF16, L.BF16, 4096, 4096, 4096, P, P, P)
-    assert c2["family"] in ("pipe", "wave") and (c2["tile_m"], c2["tile_n"]) == (256, 256) and c2["workgroups"] == 256
+    assert c2["family"] == "wave" and (c2["tile_m"], c2["tile_n"]) == (256, 256) and c2["workgroups"] == 256
     c4 = choose(L.I8, L.BF16, 4096, 4096, 4096, P, P, P, row_scale=P, col_scale=P)
-    assert c4["family"] in ("pipe", "wave") and "i8" in c4["name"]
-    assert choose(L.I8, L.I32, 4096, 4096, 4096, P, P, P)["family"] in ("pipe", "wave")
+    assert c4["family"] == "wave" and "i8" in c4["name"]
+    assert choose(L.I8, L.I32, 4096, 4096, 4096, P, P, P)["family"] == "wave"
     for m in (1, 4, 16):
         assert choose(L.BF16, L.BF16, m, 14336, 4096, P, P, P, trans_b=True)["family"] == "skinny"
     fwd = choose(L.BF16, L.BF16, 8192, 11008, 4096, P, P, P, bias=P, bias_type=L.BF16, act=L.ACT_GELU)
@@ -167,7 +210,7 @@ def test_the_selector_refuses_what_no_kernel_computes():
     assert status(ab_type=L.I8, c_type=L.I32, act=L.ACT_RELU) == L.E_TYPE  # the accumulator itself, no epilogue
     assert status(lda=63) == L.E_SHAPE  # a row of 64 needs lda >= 64
     assert status(kernel=9999) == L.E_KERNEL
-    assert status(k=60, kernel=L.kernel_named("cairn_pipe_bf16_nn_256x256")) == L.E_KERNEL  # k % 8
+    assert status(k=60, kernel=L.kernel_named("cairn_wave_bf16_nn_256x256")) == L.E_KERNEL  # k % 8
     assert status(c=None) == L.E_ARG
     assert status(act=7) == L.E_ARG
     bad = L.desc(L.BF16, L.F32, 64, 64, 64, P, P, P)
@@ -181,9 +224,7 @@ def test_the_kernel_table_is_consistent():
     assert len({k["name"] for k in ks}) == len(ks)
     for k in ks:
         assert k["lds_bytes"] <= 160 * 1024, k
-        assert k["family"] in ("mfma", "pipe", "wave", "generic", "skinny")
-        if k["family"] == "pipe":
-            assert k["threads"] == 512 and k["tile_k"] in (32, 64)
+        assert k["family"] in ("mfma", "wave", "generic", "skinny")
         if k["family"] == "wave":
             assert k["threads"] == 256 and k["tile_k"] in (32, 64)
 

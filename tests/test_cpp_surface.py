@@ -1,6 +1,7 @@
-"""The C++ surface in include/cairn, built with g++ on the host (tests/cpp/surface.cpp) under a recording machine:
-the execution context's rules, its traps, and the storage floats and host multiply bit for bit against the
-reference's own outputs (tests/golden/reference.npz)."""
+"""The C++ surface in include/cairn, built with g++ on the host under the address and undefined-behaviour sanitizers:
+tests/cpp/surface.cpp under a recording machine (the execution context's rules, its traps, and the storage floats and
+host multiply bit for bit against the reference's own outputs, tests/golden/reference.npz), and tests/cpp/emitted.cpp,
+an emitted-shaped unit, linked against the library and built emulated (-DCAIRN_EMULATE) and run."""
 
 from __future__ import annotations
 
@@ -13,14 +14,15 @@ import pytest
 ROOT = Path(__file__).resolve().parents[1]
 GOLDEN = np.load(ROOT / "tests" / "golden" / "reference.npz")
 FORMATS = ["f16", "bf16", "f8e4m3", "f8e5m2"]
+SANITIZED = ["-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all"]
 
 
 @pytest.fixture(scope="module")
 def surface(tmp_path_factory) -> Path:
     exe = tmp_path_factory.mktemp("surface") / "surface"
-    subprocess.run(["g++", "-std=c++20", "-O1", "-ffp-contract=off", "-Wall", "-Wextra", "-Werror",
-                    f"-I{ROOT / 'include'}", str(ROOT / "tests" / "cpp" / "surface.cpp"), "-o", str(exe)],
-                   check=True)  # fmt: skip
+    subprocess.run(["g++", "-std=c++20", *SANITIZED, "-ffp-contract=off", "-Wall", "-Wextra", "-Werror",
+                    "-DCAIRN_GEMM_UNLINKED=1", f"-I{ROOT / 'include'}", str(ROOT / "tests" / "cpp" / "surface.cpp"),
+                    "-o", str(exe)], check=True)  # fmt: skip
     return exe
 
 
@@ -30,13 +32,13 @@ def run(exe: Path, *args: str) -> subprocess.CompletedProcess:
 
 def test_the_context_keeps_the_reference_rules(surface):
     done = run(surface, "context")
-    assert done.returncode == 0, done.stdout + done.stderr
+    assert done.returncode == 0 and "Sanitizer" not in done.stderr, done.stdout + done.stderr
     lines = done.stdout.splitlines()
-    assert lines[-1] == "0 failures" and sum(line.startswith("ok ") for line in lines) >= 30
+    assert lines[-1] == "0 failures" and sum(line.startswith("ok ") for line in lines) >= 40
 
 
 @pytest.mark.parametrize("case", ["shape", "nested", "settle", "observe", "leaked", "lease", "unleased", "ticket",
-                                  "overflow", "e4m3", "scale"])
+                                  "rebind", "overflow", "e4m3", "scale"])
 def test_misuse_traps(surface, case):
     done = run(surface, "trap", case)
     assert done.returncode == -6 and "returned" not in done.stdout, (done.returncode, done.stdout)
@@ -94,3 +96,19 @@ def test_emitted_code_builds_against_the_include_set_and_the_library(tmp_path):
     syms = subprocess.run(["nm", str(exe)], capture_output=True, text=True, check=True).stdout
     assert "cf_emitted_mma" in syms and "cq_emitted_mma" in syms
     assert "cairn_gemm_mma" in subprocess.run(["nm", "-u", str(exe)], capture_output=True, text=True).stdout
+
+
+def test_emitted_code_runs_emulated_as_the_host_multiply(tmp_path):
+    """`cairn build --emulate` (src/cairn/projects/toolchain.py:175-180): the emitted-shaped unit built by the host
+    compiler with -DCAIRN_EMULATE, no library and no GPU. launch<A> on the emulated machine is the host loop
+    (src/cairn/runtime/cairn_emulate.hpp:151-156), bit for bit, for every storage float on the reference's device
+    shapes; the C entries run held and enqueued; a descriptor's GEMM follows its stated steps."""
+    exe = tmp_path / "emulated"
+    subprocess.run(["g++", "-std=c++20", *SANITIZED, "-ffp-contract=off", "-fno-exceptions", "-fno-rtti", "-Wall",
+                    "-Wextra", "-Werror", "-DCAIRN_EMULATE", f"-I{ROOT / 'include' / 'cairn'}",
+                    str(ROOT / "tests" / "cpp" / "emitted.cpp"), "-o", str(exe)], check=True)  # fmt: skip
+    assert "cairn_gemm" not in subprocess.run(["nm", "-u", str(exe)], capture_output=True, text=True).stdout
+    done = run(exe)
+    assert done.returncode == 0 and "Sanitizer" not in done.stderr, done.stdout + done.stderr
+    lines = done.stdout.splitlines()
+    assert lines[-1] == "0 failures" and sum(line.startswith("ok ") for line in lines) == 6

@@ -1,4 +1,4 @@
-"""The HIP execution layer on the GPU (include/cairn/cairn_hip_exec.hpp over cairn_context.hpp), through the scenario
+"""The HIP execution layer on the GPU (include/cairn/cairn_ops.hpp and cairn_hip_kernels.hpp over cairn_context.hpp), through the scenario
 programs of tests/cpp/exec_device.hip: the device half of the execution-context row (the reference's
 src/cairn/runtime/cairn_exec.hpp:25-230, cairn_reuse.hpp:1-525, cairn_gpu.hpp:47-126). Each result is checked
 against numpy; the integer folds are exact, so any association order the device library picks gives the same
@@ -41,7 +41,7 @@ def ptr(a: np.ndarray) -> int:
     return a.ctypes.data
 
 
-@pytest.mark.parametrize("n", [1, 1000, 65536 * 4 + 37])
+@pytest.mark.parametrize("n", [1, 1000, 65536 * 4 + 37, (1 << 23) + 12345])
 def test_regions_reductions_scans_and_plans(ex, n):
     sums = np.zeros(4, np.int64)
     inc, exc, kept = (np.zeros(n, np.int64) for _ in range(3))

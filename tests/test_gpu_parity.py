@@ -88,7 +88,7 @@ def test_the_tile_simulator_shapes_equal_the_host_loop_for_every_kernel():
     """Every tiled kernel (each layout, tile and operand size) on shapes with tails, exact data. A kernel the selector
     refuses for a shape (the one-wave-a-SIMD kernel needs long enough rows) skips it, but runs at least two."""
     for info in L.kernels():
-        if info["family"] not in ("mfma", "pipe", "wave"):
+        if info["family"] not in ("mfma", "wave"):
             continue
         ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
         shapes = [(16, 16, 16), (info["tile_m"] + 16, info["tile_n"] + 32, 200), (272, 144, 72), (264, 264, 104),
@@ -123,7 +123,7 @@ def test_every_ring_kernel_rounds_its_own_f32_result_to_bf16():
     kernel computes in f32: the fast store path and the general one agree bit for bit."""
     rng = np.random.default_rng(77)
     for info in L.kernels():
-        if info["family"] not in ("pipe", "wave") or info["ab_type"] != L.BF16:
+        if info["family"] != "wave" or info["ab_type"] != L.BF16:
             continue
         ta, tb = info["trans_a"], info["trans_b"]
         m, n, k = info["tile_m"] + 40, info["tile_n"] + 24, 136
@@ -142,7 +142,7 @@ def test_every_ring_kernel_applies_the_epilogue_in_its_stated_order(act):
     rng = np.random.default_rng(78 + act)
     ran = 0
     for info in L.kernels():
-        if info["family"] not in ("pipe", "wave"):
+        if info["family"] != "wave":
             continue
         ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
         m, n, k = info["tile_m"] + 40, info["tile_n"] + 24, 144
@@ -173,7 +173,7 @@ def test_every_ring_kernel_applies_the_epilogue_in_its_stated_order(act):
     assert ran >= 10
 
 
-@pytest.mark.parametrize("name", ["cairn_pipe_bf16_nn_256x256", "cairn_wave_bf16_nn_256x256"])
+@pytest.mark.parametrize("name", ["cairn_wave_bf16_nn_256x256"])
 def test_bf16_outputs_round_ties_to_even_keep_subnormals_and_overflow(name):
     """Outputs exact in f32 that sit on bf16 rounding ties: near 1 (c = b0 +- 2^-8), among the subnormals
     (c = 2^-127 b0, spacing 2^-133 against f32's 2^-149) and at the top (c = 2^127 (b0 + 2^-8), whose last tie rounds
@@ -220,7 +220,7 @@ def test_random_operands_keep_the_contract_on_every_layout(fmt, trans_a, trans_b
         exact, mag = H.exact_product(A, B)
         c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
         got, ch = run_gemm(fmt, L.F32, m, n, k, a, b, c0, trans_a=trans_a, trans_b=trans_b, accumulate=True)
-        assert ch["family"] in ("mfma", "pipe", "wave")
+        assert ch["family"] in ("mfma", "wave")
         assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
         # bf16 output: the contract plus half an ulp of the output format.
         got16, _ = run_gemm(fmt, L.BF16, m, n, k, a, b, trans_a=trans_a, trans_b=trans_b)
@@ -453,3 +453,83 @@ def test_the_mlp_layer_at_full_size_keeps_the_contract():
     exact, mag = H.exact_product(xv[:, wrows].T, dyv)
     room = H.bound(m, np.zeros(1), mag) + 2.0**-8 * np.abs(exact) * 1.01
     assert H.outside(H.f32_from_bf16(dw[wrows]), exact, room) == 0
+
+
+# ------------------------------------------------------------------ padded leading dimensions
+
+
+def padded(x: np.ndarray, ld: int, fill=0) -> np.ndarray:
+    """x (rows x cols) stored with `ld` elements a row; the padding holds `fill`."""
+    out = np.full((x.shape[0], ld), fill, dtype=x.dtype)
+    out[:, : x.shape[1]] = x
+    return out
+
+
+@pytest.mark.parametrize("ldc_pad", [4, 8])
+def test_padded_leading_dimensions_on_every_tiled_kernel(ldc_pad):
+    """Every tiled kernel with lda and ldb 16 elements past their rows and ldc = n + 4 (bf16 rows of c on 8 bytes:
+    the checked 8-byte stores) or n + 8 (on 16 bytes: the LDS-staged 16-byte stores), on whole tiles and on tails.
+    Exact data, so a bf16 output is the exact sum rounded once, and int8 is exact both as int32 and through unit
+    dequant scales into bf16; the padding of c keeps its bytes."""
+    ran = 0
+    for info in L.kernels():
+        if info["family"] not in ("mfma", "wave"):
+            continue
+        ta, tb, t = info["trans_a"], info["trans_b"], info["ab_type"]
+        for m, n, k in [(2 * info["tile_m"], 2 * info["tile_n"], 256), (info["tile_m"] + 40, info["tile_n"] + 24, 208)]:
+            arow, brow = (m if ta else k), (k if tb else n)
+            lda, ldb, ldc = arow + 16, brow + 16, n + ldc_pad
+            d = L.desc(t, L.I32 if t == L.I8 else L.BF16, m, n, k, 1 << 20, 1 << 20, 1 << 20, trans_a=ta, trans_b=tb,
+                       lda=lda, ldb=ldb, ldc=ldc, kernel=info["id"])  # fmt: skip
+            if L.load().cairn_gemm_select(C.byref(d), None) != L.OK:
+                continue
+            if t == L.I8:
+                a = (H.tile_values(m * k, 3 + m) * 16).astype(np.int8).reshape((k, m) if ta else (m, k))
+                b = (H.tile_values(k * n, 5 + n) * 16).astype(np.int8).reshape((n, k) if tb else (k, n))
+                exact = H.gemm_i8(m, n, k, a, b, trans_a=ta, trans_b=tb).astype(np.float64)
+                outs = [(L.I32, np.int32, 0x5A5A5A5A), (L.BF16, np.uint16, 0x7A7A)]
+            else:
+                a = H.encode(t, H.tile_values(m * k, 3 + m)).reshape((k, m) if ta else (m, k))
+                b = H.encode(t, H.tile_values(k * n, 5 + n)).reshape((n, k) if tb else (k, n))
+                exact, _ = H.gemm_f64(t, m, n, k, a, b, trans_a=ta, trans_b=tb)
+                outs = [(L.BF16, np.uint16, 0x7A7A)]
+            ap, bp = padded(a, lda), padded(b, ldb)
+            for out_type, out_dtype, sentinel in outs:
+                say(f"padded {info['name']} {m}x{n}x{k} lda {lda} ldb {ldb} ldc {ldc} -> {L.TYPE_NAMES[out_type]}")
+                c_host = np.full((m, ldc), sentinel, dtype=out_dtype)
+                ones_m, ones_n = np.ones(m, np.float32), np.ones(n, np.float32)
+                scaled = t == L.I8 and out_type == L.BF16
+                bufs = [hip.Buffer.of(x) for x in (ap, bp, c_host, ones_m, ones_n)]
+                d = L.desc(t, out_type, m, n, k, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, trans_a=ta, trans_b=tb,
+                           lda=lda, ldb=ldb, ldc=ldc, kernel=info["id"], row_scale=bufs[3].ptr if scaled else None,
+                           col_scale=bufs[4].ptr if scaled else None)  # fmt: skip
+                L.run(d)
+                hip.synchronize()
+                got = bufs[2].download(c_host.shape, out_dtype)
+                for x in bufs:
+                    x.close()
+                if out_type == L.I32:
+                    assert np.array_equal(got[:, :n].astype(np.float64), exact), (info["name"], m, n, k, ldc)
+                else:
+                    want = H.bf16_from_f32(exact.astype(np.float32))
+                    assert np.array_equal(got[:, :n], want), (info["name"], m, n, k, ldc)
+                assert np.all(got[:, n:] == out_dtype(sentinel)), (info["name"], "wrote into the padding of c")
+                ran += 1
+    assert ran >= 20
+
+
+def test_w8a8_with_its_fused_dequant_at_4096_cubed():
+    """C4 whole: int8 4096^3 with per-row and per-column f32 scales U[1e-3, 1e-2] fused into the epilogue, bf16 out.
+    512 sampled rows against the oracle's dequant of the exact int32 sums (bf16((f32(acc) * sa[i]) * sb[j])), bit
+    for bit."""
+    rng = np.random.default_rng(44096)
+    n = 4096
+    a = rng.integers(-127, 128, (n, n), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, n), dtype=np.int8)
+    sa = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    sb = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    got, ch = run_gemm(L.I8, L.BF16, n, n, n, a, b, row_scale=sa, col_scale=sb)
+    say("W8A8 4096^3 ran on", ch["name"])
+    rows = np.sort(rng.choice(n, 512, replace=False))
+    acc = (a[rows].astype(np.float64) @ b.astype(np.float64)).astype(np.int32)  # exact: |sums| < 2^26
+    assert np.array_equal(got[rows], H.dequant(acc, sa[rows], sb)), "dequant differs from the oracle's order"

@@ -1,4 +1,4 @@
-"""What the one-wave-a-SIMD kernel (cairn_amd/csrc/gemm_wave.hip) needs of the compiler, checked on its gfx950
+"""What the one-wave-a-SIMD kernel (cairn_amd/csrc/wave.hpp, instances in gemm_wave_<type>.hip) needs of the compiler, checked on its gfx950
 assembly: M0 holds the LDS base of a group of loads and each load picks its KiB by immediate offset, so between a write
 of M0 and the loads of its group nothing may write M0 again. The kernel writes M0 in inline assembly the compiler
 cannot see into; this test reads what the compiler emitted and holds it to that. No GPU is used: hipcc cross-compiles.
@@ -22,10 +22,13 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-S", "--cuda-device-only
 def assembly(tmp_path_factory) -> str:
     if not shutil.which("hipcc"):
         pytest.skip("hipcc is not installed")
-    out = tmp_path_factory.mktemp("isa") / "wave.s"
-    subprocess.run(["hipcc", *FLAGS, str(ROOT / "cairn_amd" / "csrc" / "gemm_wave.hip"), "-o", str(out)], check=True,
-                   capture_output=True, timeout=600)  # fmt: skip
-    return out.read_text()
+    where = tmp_path_factory.mktemp("isa")
+    texts = []
+    for src in sorted((ROOT / "cairn_amd" / "csrc").glob("gemm_wave_*.hip")):
+        out = where / (src.stem + ".s")
+        subprocess.run(["hipcc", *FLAGS, str(src), "-o", str(out)], check=True, capture_output=True, timeout=600)
+        texts.append(out.read_text())
+    return "\n".join(texts)
 
 
 def kernels(asm: str) -> dict[str, list[str]]:
@@ -38,7 +41,7 @@ def kernels(asm: str) -> dict[str, list[str]]:
 
 def test_every_lds_load_group_starts_with_its_own_base(assembly):
     ks = kernels(assembly)
-    assert len(ks) >= 14
+    assert len(ks) >= 20
     for name, lines in ks.items():
         groups, current = [], None
         for line in lines:
