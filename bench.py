@@ -191,17 +191,58 @@ def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
     if family:
         for d, lay in ((fwd, "nn"), (bwd_x, "nt"), (bwd_w, "tn")):
             d.kernel = L.kernel_named(f"cairn_{family}_bf16_{lay}_256x256")
-    out = {}
+    # One workspace for the split last rounds, shared: the three GEMMs run one after another on one stream.
+    need = max(L.workspace(d) for d in (fwd, bwd_x, bwd_w))
+    ws = hip.Buffer(max(need, 256))
+    for d in (fwd, bwd_x, bwd_w):
+        d.workspace, d.workspace_bytes = ws.ptr, need
+    out = {"workspace_bytes": need}
     flops = 2.0 * M * K * N
+    launches = max(steps, 50)
     for name, d in (("fwd", fwd), ("dx", bwd_x), ("dw", bwd_w)):
-        t = timed([d], stream, max(steps // 4, 5), warmup)
-        out[name] = {"kernel": L.select(d)["name"], "tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12, **t}
-        log(f"mlp {name}: {out[name]['tflops']:.0f} TFLOP/s on {out[name]['kernel']}")
-    t = timed([fwd, bwd_x, bwd_w], stream, 3 * max(steps // 4, 5), warmup)
+        ch = L.select(d)
+        t = timed([d], stream, launches, warmup)
+        whole = L.Desc.from_buffer_copy(d)
+        whole.split_units = -1  # the same GEMM with its last round run whole, for comparison
+        tw = timed([whole], stream, launches, warmup // 2)
+        out[name] = {"kernel": ch["name"], "tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
+                     "split_tiles": ch["split_tiles"], "split_units": ch["split_units"],
+                     "efficiency": round(ch["efficiency"], 4),
+                     "tflops_whole_rounds": flops / (tw["event_ms_per_step"] * 1e-3) / 1e12, **t}  # fmt: skip
+        log(f"mlp {name}: {out[name]['tflops']:.0f} TFLOP/s on {ch['name']} (split {ch['split_tiles']} tiles; "
+            f"whole rounds {out[name]['tflops_whole_rounds']:.0f})")  # fmt: skip
+    t = timed([fwd, bwd_x, bwd_w], stream, 3 * launches, warmup)
     out["step_ms"] = 3 * t["event_ms_per_step"]
     out["tflops"] = 3 * flops / (out["step_ms"] * 1e-3) / 1e12
-    for b in (x, w, bias, dy, y, dx, dw):
+    for b in (x, w, bias, dy, y, dx, dw, ws):
         b.close()
+    return out
+
+
+def bench_split(stream, steps, warmup) -> dict:
+    """The split last round where the selector takes it: 2048 x 8448 x 8192 bf16 (264 tiles: one round, then one tile
+    an XCD over 256 stages), with the workspace it asks for and with none."""
+    rng = np.random.default_rng(11)
+    m, n, k = 2048, 8448, 8192
+    a = hip.Buffer.of(operands(L.BF16, (m, k), rng))
+    b = hip.Buffer.of(operands(L.BF16, (k, n), rng))
+    c = hip.Buffer(m * n * 2)
+    d = L.desc(L.BF16, L.BF16, m, n, k, a.ptr, b.ptr, c.ptr)
+    need = L.workspace(d)
+    ws = hip.Buffer(max(need, 256))
+    d.workspace, d.workspace_bytes = ws.ptr, need
+    ch = L.select(d)
+    flops = 2.0 * m * n * k
+    t = timed([d], stream, max(steps, 50), warmup)
+    whole = L.Desc.from_buffer_copy(d)
+    whole.split_units = -1
+    tw = timed([whole], stream, max(steps, 50), warmup // 2)
+    out = {"problem": f"{m}x{n}x{k} bf16 NN", "split_tiles": ch["split_tiles"], "split_units": ch["split_units"],
+           "workspace_bytes": need, "tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
+           "tflops_whole_rounds": flops / (tw["event_ms_per_step"] * 1e-3) / 1e12}  # fmt: skip
+    log(f"split {out['problem']}: {out['tflops']:.0f} TFLOP/s split, {out['tflops_whole_rounds']:.0f} whole")
+    for x in (a, b, c, ws):
+        x.close()
     return out
 
 
@@ -395,7 +436,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=400)
-    ap.add_argument("--only", choices=["square", "skinny", "mlp", "quantize", "all", "traffic", "calibrate"], default="all")
+    ap.add_argument("--only", choices=["square", "skinny", "mlp", "split", "quantize", "all", "traffic", "calibrate"],
+                    default="all")  # fmt: skip
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--family", choices=["wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
@@ -446,6 +488,8 @@ def main() -> int:
         record["skinny"] = bench_skinny(stream, args.steps, args.warmup)
     if args.only in ("mlp", "all"):
         record["mlp"] = bench_mlp(stream, args.steps, args.warmup, args.family)
+    if args.only in ("split", "all"):
+        record["split"] = bench_split(stream, args.steps, args.warmup)
     if args.only in ("quantize", "all"):
         record["quantize"] = bench_quantize(stream, args.steps, args.warmup)
     record["device"] = dev

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstddef>
 #include <cstring>
 #include "../../include/cairn_gemm.h"
 #include "kernels.hpp"
@@ -26,6 +27,7 @@ int cairn_skinny_width(int n);
 namespace {
 
 constexpr int CUS = 256;              // gfx950: 8 XCDs of 32 CUs (MI350X, MI355X)
+constexpr int XCDS = 8;
 constexpr int LDS_PER_CU = 160 * 1024;
 
 enum Family { MFMA = 0, GENERIC = 1, SKINNY = 2, WAVE = 4 };  // 3 was an eight-wave kernel, retired
@@ -75,8 +77,12 @@ struct Problem {
 };
 
 int check(const cairn_gemm_desc* in, Problem& out) {
-  if(!in || in->version != CAIRN_GEMM_DESC_VERSION) return CAIRN_E_ARG;
-  cairn_gemm_desc d = *in;
+  if(!in || (in->version != 1u && in->version != CAIRN_GEMM_DESC_VERSION)) return CAIRN_E_ARG;
+  // A version 1 descriptor ends at `kernel`: the fields after it are not read, and it never splits.
+  cairn_gemm_desc d{};
+  std::memcpy(&d, in, in->version == 1u ? offsetof(cairn_gemm_desc, workspace) : sizeof(d));
+  if(in->version == 1u) d.split_units = -1;
+  if(d.split_units < -1 || (d.workspace && reinterpret_cast<std::uintptr_t>(d.workspace) % 256)) return CAIRN_E_ARG;
   const int t = d.ab_type;
   if(t != CAIRN_TYPE_F16 && t != CAIRN_TYPE_BF16 && t != CAIRN_TYPE_F8E4M3 && t != CAIRN_TYPE_F8E5M2 &&
      t != CAIRN_TYPE_I8)
@@ -192,12 +198,65 @@ int tile_k(const Kernel& k) {
   return byte ? bytes : bytes / 2;
 }
 
+// The split last round a ring kernel would run for d with `room` workspace bytes (cairn::tile::Split). The tile ids
+// are dealt to the 8 XCDs in blocks (where the tile count divides into 8 blocks; else one block); each block keeps
+// whole rounds of its XCD's CUs for the whole-tile pass and splits the rest. No split where the blocks are whole
+// rounds, a split is not asked for or would not pay (below), or the room holds too few units; the selector's choice takes a unit a CU, as many as the room holds, and no unit with
+// fewer than SPLIT_MIN stages (a segment pays its own prologue and a partial tile's stores). A split asked for
+// explicitly (split_units > 0, for the whole machine) that cannot run is refused instead.
+struct Plan {
+  std::uint64_t whole;  // workgroups of the whole-tile pass
+  cairn::tile::Split split;
+  std::uint64_t bytes;  // workspace the split uses
+  int status;
+};
+Plan plan_of(const cairn_gemm_desc& d, const Kernel& k, std::uint64_t room) {
+  const std::uint64_t tiles = ((d.m + k.bm - 1) / k.bm) * ((d.n + k.bn - 1) / k.bn);
+  const int xcds = tiles % XCDS == 0 ? XCDS : 1;
+  const std::uint64_t block = tiles / xcds, per = CUS / xcds;  // ids and CUs an XCD block has
+  Plan pl{tiles, {}, 0, CAIRN_OK};
+  pl.split.first = int(block);
+  pl.split.xcds = xcds;
+  pl.split.block = int(block);
+  const bool asked = d.split_units > 0;
+  if(!ring(k) || d.split_units < 0 || d.k == 0) return pl;
+  const std::uint64_t first = block / per * per, left = block - first;
+  const std::uint64_t stages = (d.k + tile_k(k) - 1) / tile_k(k), slot = std::uint64_t(k.bm) * k.bn * 4;
+  if(!left) return pl;
+  constexpr std::uint64_t SPLIT_MIN = 8;
+  const std::uint64_t units = asked ? std::max<std::uint64_t>(1, std::uint64_t(d.split_units) / xcds)
+                                    : std::min({per, room / (2 * slot * xcds), (left * stages) / SPLIT_MIN});
+  if(!units) return pl;
+  const std::uint64_t quota = (left * stages + units - 1) / units;
+  if(quota > stages) {  // a unit would reach into a third tile
+    if(asked) pl.status = CAIRN_E_ARG;
+    return pl;
+  }
+  // The selector splits only a last round that would keep at most a quarter of the XCD's CUs busy, over at least 16
+  // stages. Measured on the MLP layer's shapes (5.375 and 2.69 rounds), a split round was slower than the whole one:
+  // CUs left idle let the power-limited clock rise, so a partial round costs far less than a full one (96 of 256
+  // tiles: 0.57 of a full round's time), while split units each fetch their own panels, with no reuse across tiles
+  // in L2, and write partial tiles the fixup reads back.
+  if(!asked && (stages < 16 || 4 * left > per || 4 * quota > 3 * stages)) return pl;
+  const std::uint64_t used = (left * stages + quota - 1) / quota;  // units an XCD runs
+  const std::uint64_t bytes = 2 * xcds * used * slot;
+  if(bytes > room) {
+    if(asked) pl.status = CAIRN_E_SCRATCH;
+    return pl;
+  }
+  pl.whole = xcds * first;
+  pl.split = cairn::tile::Split{int(first), int(left), int(stages), int(quota), int(used), xcds, int(block)};
+  pl.bytes = bytes;
+  return pl;
+}
+std::uint64_t room_of(const cairn_gemm_desc& d) { return d.workspace ? d.workspace_bytes : 0; }
+
 struct Estimate {
   double cost, waves, efficiency;
   std::uint64_t workgroups;
 };
 
-Estimate estimate(const cairn_gemm_desc& d, const Kernel& k) {
+Estimate estimate(const cairn_gemm_desc& d, const Kernel& k, const Plan& plan) {
   Estimate e{};
   if(k.family == SKINNY) {
     const std::uint64_t width = std::uint64_t(cairn_skinny_width(int(d.n)));
@@ -210,8 +269,10 @@ Estimate estimate(const cairn_gemm_desc& d, const Kernel& k) {
   }
   const std::uint64_t tm = (d.m + k.bm - 1) / k.bm, tn = (d.n + k.bn - 1) / k.bn;
   const std::uint64_t tiles = tm * tn, slots = std::uint64_t(CUS) * resident(k);
-  const double rounds = std::ceil(double(tiles) / double(slots));
-  e.workgroups = tiles;
+  // A split last round costs a unit's share of a tile's stages instead of a whole round.
+  const double rounds = plan.split.tiles ? double(plan.whole / slots) + double(plan.split.quota) / plan.split.stages
+                                         : std::ceil(double(tiles) / double(slots));
+  e.workgroups = plan.split.tiles ? plan.whole + std::uint64_t(plan.split.xcds) * plan.split.units : tiles;
   e.waves = double(tiles) / double(slots);
   // Time: rounds of resident tiles, each round a tile's k-loop at the shape's rate (resident tiles share a CU).
   e.cost = rounds * double(k.bm) * double(k.bn) * resident(k) / shape_rate(k);
@@ -239,7 +300,7 @@ int choose(const cairn_gemm_desc& d, int named) {
   for(int id = 1; id <= COUNT; ++id) {
     const Kernel& k = TABLE[id - 1];
     if(!tiled_fits(d, k)) continue;
-    const double c = estimate(d, k).cost;
+    const double c = estimate(d, k, plan_of(d, k, room_of(d))).cost;
     if(!best || c < cost) best = id, cost = c;
   }
   if(best) return best;
@@ -248,8 +309,11 @@ int choose(const cairn_gemm_desc& d, int named) {
   return -CAIRN_E_KERNEL;
 }
 
-Params params_of(const cairn_gemm_desc& d, const Kernel& k) {
+Params params_of(const cairn_gemm_desc& d, const Kernel& k, const Plan& plan) {
   Params p{};
+  p.whole_tiles = int(plan.whole);
+  p.split = plan.split;
+  p.work = d.workspace;
   p.a = d.a;
   p.b = d.b;
   p.c = d.c;
@@ -316,6 +380,7 @@ const char* cairn_gemm_status_string(int status) {
     case CAIRN_E_KERNEL: return "the kernel named cannot run this problem";
     case CAIRN_E_ARG: return "a required pointer is null or the descriptor is malformed";
     case CAIRN_E_HIP: return "the HIP runtime refused the launch";
+    case CAIRN_E_SCRATCH: return "the split last round asked for needs more scratch than the workspace holds";
     default: return "unknown status";
   }
 }
@@ -325,10 +390,15 @@ int cairn_gemm_select(const cairn_gemm_desc* desc, cairn_gemm_choice* out) {
   if(const int s = check(desc, pr)) return s;
   const int id = choose(pr.d, desc->kernel);
   if(id < 0) return -id;
+  const Kernel& k = TABLE[id - 1];
+  const Plan plan = plan_of(pr.d, k, room_of(pr.d));
+  if(plan.status) return plan.status;
   if(out) {
-    const Kernel& k = TABLE[id - 1];
-    const Estimate e = estimate(pr.d, k);
+    const Estimate e = estimate(pr.d, k, plan);
     std::memset(out, 0, sizeof(*out));
+    out->split_tiles = plan.split.xcds * plan.split.tiles;
+    out->split_units = plan.split.xcds * plan.split.units;
+    out->split_bytes = plan.bytes;
     out->kernel = id;
     out->family = k.family;
     out->tile_m = k.bm;
@@ -341,6 +411,17 @@ int cairn_gemm_select(const cairn_gemm_desc* desc, cairn_gemm_choice* out) {
   return CAIRN_OK;
 }
 
+int cairn_gemm_workspace(const cairn_gemm_desc* desc, uint64_t* bytes) {
+  Problem pr;
+  if(const int s = check(desc, pr)) return s;
+  const int id = choose(pr.d, desc->kernel);
+  if(id < 0) return -id;
+  const Plan plan = plan_of(pr.d, TABLE[id - 1], ~std::uint64_t(0));
+  if(plan.status) return plan.status;
+  if(bytes) *bytes = pr.empty ? 0 : plan.bytes;
+  return CAIRN_OK;
+}
+
 int cairn_gemm_run(const cairn_gemm_desc* desc, void* stream) {
   Problem pr;
   if(const int s = check(desc, pr)) return s;
@@ -348,7 +429,9 @@ int cairn_gemm_run(const cairn_gemm_desc* desc, void* stream) {
   if(id < 0) return -id;
   if(pr.empty) return CAIRN_OK;
   const Kernel& k = TABLE[id - 1];
-  const Params p = params_of(pr.d, k);
+  const Plan plan = plan_of(pr.d, k, room_of(pr.d));
+  if(plan.status) return plan.status;
+  const Params p = params_of(pr.d, k, plan);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if(k.family == GENERIC) e = cairn_generic(p, s);

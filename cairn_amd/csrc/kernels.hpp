@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include "../../include/cairn_gemm.h"
+#include "tile.hpp"
 
 namespace cairn::gemm {
 
@@ -31,6 +32,9 @@ struct Params {
   const float* row_scale;
   const float* col_scale;
   int rows16;            // every row of c starts on 16 bytes (c 16-byte aligned, ldc a multiple of 16 bytes)
+  int whole_tiles;       // workgroups of the whole-tile pass (workgroup b: tile id whole_id(split, b))
+  cairn::tile::Split split;  // the split last round (split.tiles 0: none)
+  void* work;            // the split round's partial tiles: 2 split.units slots of BM x BN 32-bit values
 };
 
 __device__ inline std::uint32_t as_bits(float x) { return __builtin_bit_cast(std::uint32_t, x); }

@@ -118,15 +118,69 @@ CAIRN_HD int acc_n(int lane, int q) { return 8 * q + 4 * (lane >> 5); }
 // and each XCD has its own L2, so ids are first remapped to give each XCD a contiguous run; ids then walk `group`
 // tile rows at a time, column by column, so the tiles an XCD holds at once share their a and b panels. A bijection
 // of [0, tiles_m * tiles_n) onto the tiles.
-CAIRN_HD void tile_of(int b, int tiles_m, int tiles_n, int group, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  const int id = total % 8 == 0 ? (b % 8) * (total / 8) + b / 8 : b;
+// xcd_order: workgroup b of `count` to its id (a bijection of [0, count)); tile_at: an id to its tile.
+CAIRN_HD int xcd_order(int b, int count) { return count % 8 == 0 ? (b % 8) * (count / 8) + b / 8 : b; }
+CAIRN_HD void tile_at(int id, int tiles_m, int tiles_n, int group, int& tm, int& tn) {
   const int per = group * tiles_n;
   const int first = (id / per) * group;
   const int rows = tiles_m - first < group ? tiles_m - first : group;
   const int local = id - (id / per) * per;
   tm = first + local % rows;
   tn = local / rows;
+}
+CAIRN_HD void tile_of(int b, int tiles_m, int tiles_n, int group, int& tm, int& tn) {
+  tile_at(xcd_order(b, tiles_m * tiles_n), tiles_m, tiles_n, group, tm, tn);
+}
+
+// The split last round. Where the tiles are not a whole number of rounds of the machine, each XCD's block of ids
+// (xcd_order: `block` ids an XCD, `xcds` blocks) keeps its first `first` ids, whole rounds of its CUs, for the
+// whole-tile pass, and shares its remaining `tiles` ids along k among `units` workgroups that run on the same XCD,
+// so that the panels its tiles share stay in its L2: those tiles' stages, `stages` a tile, laid end to end, unit v
+// of the XCD taking the `quota` stages from v quota on. A unit's run stays within two tiles (quota <= stages), so it
+// writes at most two partial tiles. A fixup pass then adds each tile's partials in the order of their units (their
+// k order, so the bits do not depend on timing) and applies the epilogue.
+//
+// Workgroup b of the whole-tile pass (xcds * first of them) runs id whole_id(b); workgroup u of the split pass
+// (xcds * units) is unit u / xcds of XCD u % xcds (the dispatcher hands workgroup u to XCD u % 8), and its partial
+// tiles go to slots 2 u and 2 u + 1.
+struct Split {
+  int first = 0;   // ids of an XCD's block that the whole-tile pass runs
+  int tiles = 0;   // ids of an XCD's block shared along k (0: no split)
+  int stages = 0;  // k stages a tile
+  int quota = 0;   // stages a unit
+  int units = 0;   // units an XCD
+  int xcds = 1;    // XCD blocks
+  int block = 0;   // ids an XCD's block
+};
+CAIRN_HD int whole_id(const Split& s, int b) { return (b % s.xcds) * s.block + b / s.xcds; }
+// The id of split tile t of XCD x.
+CAIRN_HD int split_id(const Split& s, int x, int t) { return x * s.block + s.first + t; }
+// Segment j (0 or 1) of unit v of an XCD: its tile (0 .. tiles - 1 of the XCD's) and its stages [s0, s1) within
+// that tile; false where the unit has no such segment.
+CAIRN_HD bool split_segment(const Split& s, int v, int j, int& tile, int& s0, int& s1) {
+  const long long total = (long long)s.tiles * s.stages;
+  long long g0 = (long long)v * s.quota;
+  const long long g1 = g0 + s.quota < total ? g0 + s.quota : total;
+  if(g0 >= g1) return false;
+  if(j == 1) {
+    const long long next = (g0 / s.stages + 1) * s.stages;  // the start of the next tile
+    if(next >= g1) return false;
+    g0 = next;
+  }
+  tile = int(g0 / s.stages);
+  const long long end = (long long)(tile + 1) * s.stages < g1 ? (long long)(tile + 1) * s.stages : g1;
+  s0 = int(g0 - (long long)tile * s.stages);
+  s1 = int(end - (long long)tile * s.stages);
+  return true;
+}
+// The units of an XCD whose runs meet its tile t (first .. last, in k order), and the slot unit v of XCD x wrote its
+// part of tile t to.
+CAIRN_HD void split_units_of(const Split& s, int t, int& first, int& last) {
+  first = int((long long)t * s.stages / s.quota);
+  last = int(((long long)(t + 1) * s.stages - 1) / s.quota);
+}
+CAIRN_HD int split_slot(const Split& s, int x, int t, int v) {
+  return 2 * (v * s.xcds + x) + ((long long)v * s.quota < (long long)t * s.stages ? 1 : 0);
 }
 
 constexpr int OUTSIDE = 0x7fffffff;  // a byte offset past every resource: the load reads zero

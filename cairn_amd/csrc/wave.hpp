@@ -201,10 +201,47 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
   finish<RAW>(p, acc, row0 + wr, col0 + wc, lane);
 }
 
-template<class Sh, int OP, bool TA, bool TB, bool RAW>
-__global__ void __launch_bounds__(256) wave_gemm(Params p) {
+// An operand panel from stage s0 on: K-major rows start s0 * ROW bytes later, M/N-major ones s0 * BK k rows later;
+// the bytes to the matrix's end shrink by as much.
+template<class Sh>
+__device__ __forceinline__ cairn::tile::Panel from_stage(cairn::tile::Panel pn, bool kmajor, int s0, std::int64_t ld) {
+  const std::int64_t skip = kmajor ? std::int64_t(s0) * Sh::ROW : std::int64_t(s0) * Sh::BK * ld * Sh::ES;
+  return cairn::tile::Panel{pn.start + skip, pn.bytes - skip};
+}
+
+// The 32-bit pattern of a value (an f32 or int32 accumulator element, taken by value: a bit cast straight from an
+// element of the accumulator vector read element 0 for every element, as compiled here).
+template<class T> __device__ __forceinline__ std::uint32_t bits32(T x) {
+  static_assert(sizeof(T) == 4, "a 32-bit accumulator");
+  return __builtin_bit_cast(std::uint32_t, x);
+}
+
+// A partial tile of the split round: the accumulators' 32-bit patterns (f32 sums, or exact int32 ones) as a BM x BN
+// row-major tile at `part`, 16 bytes a quad (the fixup reads them back in the same layout).
+template<class Sh, class Acc, int FM, int FN>
+__device__ __forceinline__ void store_partial(const Acc (&acc)[FM][FN], void* part, int wr, int wc, int lane) {
+  char* base = static_cast<char*>(part);
+#pragma unroll
+  for(int i = 0; i < FM; ++i)
+#pragma unroll
+    for(int j = 0; j < FN; ++j)
+#pragma unroll
+      for(int q = 0; q < 4; ++q) {
+        const int m = wr + 32 * i + cairn::tile::acc_m(lane), n = wc + 32 * j + cairn::tile::acc_n(lane, q);
+        u32x4 w;
+#pragma unroll
+        for(int e = 0; e < 4; ++e) w[e] = bits32(acc[i][j][4 * q + e]);  // the element's value, then its pattern
+        *reinterpret_cast<u32x4*>(base + (std::int64_t(m) * Sh::BN + n) * 4) = w;
+      }
+}
+
+// One output tile (tm, tn) over the k stages from s0 on: k counts the operands' elements from stage s0 (all of k
+// for a whole tile; a segment's share in the split round). With PART the accumulators go to `part` as a partial
+// tile (store_partial), else through the epilogue into c. lds is the workgroup's ring, terms its epilogue terms.
+template<class Sh, int OP, bool TA, bool TB, bool RAW, bool PART>
+__device__ __forceinline__ void wave_tile(const Params& p, char* lds, float* terms, int tm, int tn, int s0, int k,
+                                          void* part) {
   static_assert(Sh::WAVES == 4, "one wave a SIMD");
-  constexpr int TERMS_AT = Sh::WTM * 256 * Sh::WAVES;  // the first byte of the ring the staged store leaves free
   using M = Mfma<OP>;
   using Acc = typename M::Acc;
   constexpr bool AK = !TA, BKM = TB;
@@ -212,26 +249,15 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   constexpr int LOADS = Sh::LOADS_A + Sh::LOADS_B;  // this thread's 16-byte loads a stage
   constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, READS = RA + RB;  // LDS reads a k-step
   static_assert(READS <= 32 && LOADS <= 8, "the interleave below places these between 16 MFMAs");
-  __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
-  // The epilogue's row scales, column scales and biases of the tile (3 KiB): past the staged store's part of the
-  // ring where the ring has room (a 5-stage ring), else their own array.
-  float* terms;
-  if constexpr(S * Sh::STAGE >= TERMS_AT + 3 * 1024) terms = reinterpret_cast<float*>(lds + TERMS_AT);
-  else {
-    __shared__ float own[3 * 256];
-    terms = own;
-  }
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   int wr, wc;
   wave_origin<Sh>(wave, wr, wc);
-  int tm, tn;
-  cairn::tile::tile_of(int(blockIdx.x), p.tiles_m, p.tiles_n, p.group, tm, tn);
   const int row0 = tm * Sh::BM, col0 = tn * Sh::BN;
-  const Terms mine_terms = RAW ? Terms{} : prefetch_terms<Sh>(p, row0, col0, t);
-  const cairn::tile::Panel pa = cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES);
-  const cairn::tile::Panel pb = cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES);
+  const Terms mine_terms = RAW || PART ? Terms{} : prefetch_terms<Sh>(p, row0, col0, t);
+  const cairn::tile::Panel pa = from_stage<Sh>(cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES), AK, s0, p.lda);
+  const cairn::tile::Panel pb = from_stage<Sh>(cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES), BKM, s0, p.ldb);
   const char* a = static_cast<const char*>(p.a) + pa.start;
   const char* b = static_cast<const char*>(p.b) + pb.start;
   const unsigned ring = lds_address(lds);
@@ -241,7 +267,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   Loader<Sh, Sh::BN, BKM, Dma> lb;  // the host runs this kernel only where both loaders' imm_fits holds
   la.setup(t, row0, p.m, p.lda);
   lb.setup(t, col0, p.n, p.ldb);
-  const int T = (p.k + Sh::BK - 1) / Sh::BK;
+  const int T = (k + Sh::BK - 1) / Sh::BK;
 
   Acc acc[FM][FN];
 #pragma unroll
@@ -317,13 +343,13 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   auto load_a = [&](const auto& r, int st, auto slot, auto u, auto tail) {
     constexpr int U = decltype(u)::value;
     if constexpr(U == 0) dma.set_base(LA::base(ring + unsigned(int(slot) * Sh::STAGE), wave));
-    if constexpr(decltype(tail)::value) la.template load_imm<U>(dma, r, st, p.k);
+    if constexpr(decltype(tail)::value) la.template load_imm<U>(dma, r, st, k);
     else la.template load_steady<U>(dma, r);
   };
   auto load_b = [&](const auto& r, int st, auto slot, auto u, auto tail) {
     constexpr int U = decltype(u)::value;
     if constexpr(U == 0) dma.set_base(LB::base(ring + unsigned(int(slot) * Sh::STAGE + Sh::A_BYTES), wave));
-    if constexpr(decltype(tail)::value) lb.template load_imm<U>(dma, r, st, p.k);
+    if constexpr(decltype(tail)::value) lb.template load_imm<U>(dma, r, st, k);
     else lb.template load_steady<U>(dma, r);
   };
   auto stage_a = [&](int st) {
@@ -358,7 +384,7 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   wb.advance();
   // Iterations before `steady` load only stages that end at or before k, or (where k is a whole number of stages)
   // stages past the last: their loads skip the per-chunk k check. The others load the last, partial, stage.
-  const int steady = p.k % Sh::BK == 0 ? T : (T - 1 - S > 0 ? T - 1 - S : 0);
+  const int steady = k % Sh::BK == 0 ? T : (T - 1 - S > 0 ? T - 1 - S : 0);
 
   // Placing: reads 2 X and 2 X + 1 of a k-step after MFMA X, so that they complete well before their MFMAs; load u of
   // a half stage after MFMA 4 u + 2.
@@ -417,7 +443,50 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
   for(; it < T; ++it) iteration(it, it % S, Tail{});
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
 
-  store_tile<Sh, RAW>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
+  if constexpr(PART) store_partial<Sh>(acc, part, wr, wc, lane);
+  else store_tile<Sh, RAW>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
+}
+
+// The ring and the epilogue terms (3 KiB: past the staged store's part of the ring where the ring has room, a
+// 5-stage ring, else an array of their own), declared by each kernel.
+#define CAIRN_WAVE_LDS(Sh)                                                                                          \
+  __shared__ __attribute__((aligned(1024))) char lds[Sh::STAGES * Sh::STAGE];                                     \
+  float* terms;                                                                                                   \
+  if constexpr(Sh::STAGES * Sh::STAGE >= Sh::WTM * 256 * Sh::WAVES + 3 * 1024)                                   \
+    terms = reinterpret_cast<float*>(lds + Sh::WTM * 256 * Sh::WAVES);                                            \
+  else {                                                                                                          \
+    __shared__ float own[3 * 256];                                                                                \
+    terms = own;                                                                                                  \
+  }
+
+// The whole-tile pass: workgroup b runs the tile of id whole_id(b) over all of k.
+template<class Sh, int OP, bool TA, bool TB, bool RAW>
+__global__ void __launch_bounds__(256) wave_gemm(Params p) {
+  CAIRN_WAVE_LDS(Sh)
+  int tm, tn;
+  cairn::tile::tile_at(cairn::tile::whole_id(p.split, int(blockIdx.x)), p.tiles_m, p.tiles_n, p.group, tm, tn);
+  wave_tile<Sh, OP, TA, TB, RAW, false>(p, lds, terms, tm, tn, 0, p.k, nullptr);
+}
+
+// The split round: workgroup u, unit u / xcds of XCD u % xcds, runs its one or two segments (split_segment) into
+// its partial slots 2 u and 2 u + 1.
+template<class Sh, int OP, bool TA, bool TB>
+__global__ void __launch_bounds__(256) wave_split(Params p) {
+  CAIRN_WAVE_LDS(Sh)
+  const int u = int(blockIdx.x), x = u % p.split.xcds, v = u / p.split.xcds;  // unit v of XCD x
+  for(int j = 0; j < 2; ++j) {
+    int tile, s0, s1;
+    if(!cairn::tile::split_segment(p.split, v, j, tile, s0, s1)) break;  // the same for every thread
+    if(j) {  // every wave is past its LDS reads of the first segment before the second refills the ring
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      fenced_barrier();
+    }
+    int tm, tn;
+    cairn::tile::tile_at(cairn::tile::split_id(p.split, x, tile), p.tiles_m, p.tiles_n, p.group, tm, tn);
+    const int k = (p.k < s1 * Sh::BK ? p.k : s1 * Sh::BK) - s0 * Sh::BK;
+    void* slot = static_cast<char*>(p.work) + std::int64_t(2 * u + j) * (Sh::BM * Sh::BN * 4);
+    wave_tile<Sh, OP, TA, TB, false, true>(p, lds, terms, tm, tn, s0, k, slot);
+  }
 }
 
 // The 8-bit floats on the same ring: one v_mfma_f32_32x32x64_f8f6f4 covers a whole stage (64 bytes of k), so a
@@ -427,10 +496,10 @@ __global__ void __launch_bounds__(256) wave_gemm(Params p) {
 //   the 16 MFMAs of stage it, between them the fragment reads of stage it + 1 and the loads of stage it + STAGES
 //   into the buffer stage it used (every wave has stage it in registers once past the barrier).
 // The hazards are the ones of wave_gemm, ordered by the one barrier a stage.
-template<class Sh, int OP, bool TA, bool TB>
-__global__ void __launch_bounds__(256) wave8_gemm(Params p) {
+template<class Sh, int OP, bool TA, bool TB, bool PART>
+__device__ __forceinline__ void wave8_tile(const Params& p, char* lds, float* terms, int tm, int tn, int s0, int k,
+                                           void* part) {
   static_assert(Sh::WAVES == 4 && Sh::ES == 1, "one wave a SIMD, 8-bit operands");
-  constexpr int TERMS_AT = Sh::WTM * 256 * Sh::WAVES;  // the first byte of the ring the staged store leaves free
   using M = Mfma<OP>;
   using Acc = typename M::Acc;
   constexpr bool AK = !TA, BKM = TB;
@@ -438,26 +507,15 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   constexpr int LOADS = Sh::LOADS_A + Sh::LOADS_B;
   constexpr int RA = AK ? FM : 2 * FM, RB = BKM ? FN : 2 * FN, STEP_READS = RA + RB, READS = 2 * STEP_READS;
   static_assert(READS <= 32 && Sh::LOADS_A <= 4 && Sh::LOADS_B <= 4, "the interleave below");
-  __shared__ __attribute__((aligned(1024))) char lds[S * Sh::STAGE];
-  // The epilogue's row scales, column scales and biases of the tile (3 KiB): past the staged store's part of the
-  // ring where the ring has room (a 5-stage ring), else their own array.
-  float* terms;
-  if constexpr(S * Sh::STAGE >= TERMS_AT + 3 * 1024) terms = reinterpret_cast<float*>(lds + TERMS_AT);
-  else {
-    __shared__ float own[3 * 256];
-    terms = own;
-  }
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   int wr, wc;
   wave_origin<Sh>(wave, wr, wc);
-  int tm, tn;
-  cairn::tile::tile_of(int(blockIdx.x), p.tiles_m, p.tiles_n, p.group, tm, tn);
   const int row0 = tm * Sh::BM, col0 = tn * Sh::BN;
-  const Terms mine_terms = false ? Terms{} : prefetch_terms<Sh>(p, row0, col0, t);
-  const cairn::tile::Panel pa = cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES);
-  const cairn::tile::Panel pb = cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES);
+  const Terms mine_terms = PART ? Terms{} : prefetch_terms<Sh>(p, row0, col0, t);
+  const cairn::tile::Panel pa = from_stage<Sh>(cairn::tile::panel(AK, row0, p.m, p.k, p.lda, ES), AK, s0, p.lda);
+  const cairn::tile::Panel pb = from_stage<Sh>(cairn::tile::panel(BKM, col0, p.n, p.k, p.ldb, ES), BKM, s0, p.ldb);
   const char* a = static_cast<const char*>(p.a) + pa.start;
   const char* b = static_cast<const char*>(p.b) + pb.start;
   const unsigned ring = lds_address(lds);
@@ -467,7 +525,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   Loader<Sh, Sh::BN, BKM, Dma> lb;  // the host runs this kernel only where both loaders' imm_fits holds
   la.setup(t, row0, p.m, p.lda);
   lb.setup(t, col0, p.n, p.ldb);
-  const int T = (p.k + Sh::BK - 1) / Sh::BK;
+  const int T = (k + Sh::BK - 1) / Sh::BK;
   using LA = Loader<Sh, Sh::BM, AK, Dma>;
   using LB = Loader<Sh, Sh::BN, BKM, Dma>;
   // A stage's place in the ring (a constant in the unrolled steady loop, else an int), and one operand's part of stage
@@ -478,13 +536,13 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   auto load_a = [&](const auto& r, int st, auto slot, auto u, auto tail) {
     constexpr int U = decltype(u)::value;
     if constexpr(U == 0) dma.set_base(LA::base(ring + unsigned(int(slot) * Sh::STAGE), wave));
-    if constexpr(decltype(tail)::value) la.template load_imm<U>(dma, r, st, p.k);
+    if constexpr(decltype(tail)::value) la.template load_imm<U>(dma, r, st, k);
     else la.template load_steady<U>(dma, r);
   };
   auto load_b = [&](const auto& r, int st, auto slot, auto u, auto tail) {
     constexpr int U = decltype(u)::value;
     if constexpr(U == 0) dma.set_base(LB::base(ring + unsigned(int(slot) * Sh::STAGE + Sh::A_BYTES), wave));
-    if constexpr(decltype(tail)::value) lb.template load_imm<U>(dma, r, st, p.k);
+    if constexpr(decltype(tail)::value) lb.template load_imm<U>(dma, r, st, k);
     else lb.template load_steady<U>(dma, r);
   };
   auto stage_all = [&](int st) {
@@ -561,7 +619,7 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
   wa.advance();
   wb.advance();
   unsigned records;
-  const int steady = p.k % Sh::BK == 0 ? T : (T - 1 - S > 0 ? T - 1 - S : 0);
+  const int steady = k % Sh::BK == 0 ? T : (T - 1 - S > 0 ? T - 1 - S : 0);
   // A 32x32x64 fp8 MFMA takes 64 cycles: between two, fifteen issue slots, room for two reads and the walk's work.
   static_assert(8 + Sh::LOADS_B <= 12, "MFMAs 12 .. 15 of a stage issue no load");
   auto iteration = [&](int it, auto slot, auto cur, auto tail) {
@@ -608,20 +666,129 @@ __global__ void __launch_bounds__(256) wave8_gemm(Params p) {
     else iteration(it, it % S, std::integral_constant<int, 0>{}, Tail{});
   }
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
-  store_tile<Sh, false>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
+  if constexpr(PART) store_partial<Sh>(acc, part, wr, wc, lane);
+  else store_tile<Sh, false>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
+}
+
+template<class Sh, int OP, bool TA, bool TB>
+__global__ void __launch_bounds__(256) wave8_gemm(Params p) {
+  CAIRN_WAVE_LDS(Sh)
+  int tm, tn;
+  cairn::tile::tile_at(cairn::tile::whole_id(p.split, int(blockIdx.x)), p.tiles_m, p.tiles_n, p.group, tm, tn);
+  wave8_tile<Sh, OP, TA, TB, false>(p, lds, terms, tm, tn, 0, p.k, nullptr);
+}
+
+template<class Sh, int OP, bool TA, bool TB>
+__global__ void __launch_bounds__(256) wave8_split(Params p) {
+  CAIRN_WAVE_LDS(Sh)
+  const int u = int(blockIdx.x), x = u % p.split.xcds, v = u / p.split.xcds;
+  for(int j = 0; j < 2; ++j) {
+    int tile, s0, s1;
+    if(!cairn::tile::split_segment(p.split, v, j, tile, s0, s1)) break;
+    if(j) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      fenced_barrier();
+    }
+    int tm, tn;
+    cairn::tile::tile_at(cairn::tile::split_id(p.split, x, tile), p.tiles_m, p.tiles_n, p.group, tm, tn);
+    const int k = (p.k < s1 * Sh::BK ? p.k : s1 * Sh::BK) - s0 * Sh::BK;
+    void* slot = static_cast<char*>(p.work) + std::int64_t(2 * u + j) * (Sh::BM * Sh::BN * 4);
+    wave8_tile<Sh, OP, TA, TB, true>(p, lds, terms, tm, tn, s0, k, slot);
+  }
+}
+
+// The split round's fixup: block (f, r), split tile f / xcds of XCD f % xcds (so that it runs on that XCD, whose L2
+// holds the partials its units wrote), rows 4 r .. 4 r + 3; thread th one quad (4 columns) of row 4 r + th / 64. It
+// adds the tile's partials in the order of their units (their k order), then applies the epilogue's steps and stores
+// c as the whole-tile pass would. INT: the partials are exact int32 sums (int8 operands), added as integers.
+template<int BM, int BN, bool INT>
+__global__ void __launch_bounds__(256) split_fixup(Params p) {
+  static_assert(BN == 256, "64 quads a row");
+  const int f = int(blockIdx.x), x = f % p.split.xcds, t = f / p.split.xcds;
+  const int row_in = 4 * int(blockIdx.y) + int(threadIdx.x) / 64, col_in = 4 * (int(threadIdx.x) % 64);
+  int tm, tn;
+  cairn::tile::tile_at(cairn::tile::split_id(p.split, x, t), p.tiles_m, p.tiles_n, p.group, tm, tn);
+  const int m = tm * BM + row_in, n = tn * BN + col_in;
+  if(m >= p.m || n >= p.n) return;  // n and p.n are multiples of 4: a quad is in or out whole
+  int first, last;
+  cairn::tile::split_units_of(p.split, t, first, last);
+  const std::int64_t within = (std::int64_t(row_in) * BN + col_in) * 4;
+  u32x4 sum = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.work) +
+                                             std::int64_t(cairn::tile::split_slot(p.split, x, t, first)) * (BM * BN * 4) + within);
+  for(int v = first + 1; v <= last; ++v) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.work) +
+                                                   std::int64_t(cairn::tile::split_slot(p.split, x, t, v)) * (BM * BN * 4) + within);
+#pragma unroll
+    for(int e = 0; e < 4; ++e) {
+      if constexpr(INT) sum[e] = std::uint32_t(int(sum[e]) + int(w[e]));
+      else sum[e] = as_bits(from_bits(sum[e]) + from_bits(w[e]));
+    }
+  }
+  char* c = static_cast<char*>(p.c);
+  const std::int64_t at = std::int64_t(m) * p.ldc + n;
+  if(INT && p.c_type == CAIRN_TYPE_I32) {
+    *reinterpret_cast<u32x4*>(c + at * 4) = sum;
+    return;
+  }
+  with_act(p, [&](auto act) {
+    constexpr int ACT = decltype(act)::value;
+    const float rs = p.row_scale ? p.row_scale[m] : 1.0f;
+    float v[4];
+#pragma unroll
+    for(int e = 0; e < 4; ++e) {
+      const float acc = INT ? float(int(sum[e])) : from_bits(sum[e]);
+      const float cs = p.col_scale ? p.col_scale[n + e] : 1.0f;
+      const float bs = !p.bias ? -0.0f
+                       : p.bias_type == CAIRN_TYPE_BF16 ? widen_bf16(static_cast<const std::uint16_t*>(p.bias)[n + e])
+                                                        : static_cast<const float*>(p.bias)[n + e];
+      v[e] = apply<ACT>(acc, rs, cs, bs);
+    }
+    if(p.c_type == CAIRN_TYPE_F32) {
+      float* out = reinterpret_cast<float*>(c + at * 4);
+      if(p.accumulate)
+#pragma unroll
+        for(int e = 0; e < 4; ++e) v[e] = out[e] + v[e];
+      *reinterpret_cast<float4*>(out) = float4{v[0], v[1], v[2], v[3]};
+    } else if(p.c_type == CAIRN_TYPE_BF16) {
+      *reinterpret_cast<u32x2*>(c + at * 2) = u32x2{narrow2_bf16(v[0], v[1]), narrow2_bf16(v[2], v[3])};
+    } else {
+      *reinterpret_cast<u32x2*>(c + at * 2) =
+          u32x2{std::uint32_t(narrow_f16(v[0])) | (std::uint32_t(narrow_f16(v[1])) << 16),
+                std::uint32_t(narrow_f16(v[2])) | (std::uint32_t(narrow_f16(v[3])) << 16)};
+    }
+  });
+}
+
+// A launch: the whole-tile pass (whole_tiles workgroups), then, where the last round is split, the split pass and its
+// fixup, all on the stream in order.
+template<class Sh, bool INT> hipError_t launch_fixup(const Params& p, hipStream_t s) {
+  hipLaunchKernelGGL((split_fixup<Sh::BM, Sh::BN, INT>), dim3(unsigned(p.split.xcds * p.split.tiles), unsigned(Sh::BM / 4)),
+                     dim3(256), 0, s, p);
+  return hipGetLastError();
 }
 
 template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave8(const Params& p, hipStream_t s) {
-  const unsigned grid = unsigned(p.tiles_m) * unsigned(p.tiles_n);
-  hipLaunchKernelGGL((wave8_gemm<Sh, OP, TA, TB>), dim3(grid), dim3(256), 0, s, p);
+  if(p.whole_tiles) hipLaunchKernelGGL((wave8_gemm<Sh, OP, TA, TB>), dim3(unsigned(p.whole_tiles)), dim3(256), 0, s, p);
+  if(p.split.tiles) {
+    hipLaunchKernelGGL((wave8_split<Sh, OP, TA, TB>), dim3(unsigned(p.split.xcds * p.split.units)), dim3(256), 0, s, p);
+    if(const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    return launch_fixup<Sh, false>(p, s);
+  }
   return hipGetLastError();
 }
 
 template<class Sh, int OP, bool TA, bool TB> hipError_t launch_wave(const Params& p, hipStream_t s) {
-  const unsigned grid = unsigned(p.tiles_m) * unsigned(p.tiles_n);
-  if(OP == OP_I8 && p.c_type == CAIRN_TYPE_I32)
-    hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB, OP == OP_I8>), dim3(grid), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB, false>), dim3(grid), dim3(256), 0, s, p);
+  constexpr bool INT = OP == OP_I8;
+  if(p.whole_tiles) {
+    if(INT && p.c_type == CAIRN_TYPE_I32)
+      hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB, INT>), dim3(unsigned(p.whole_tiles)), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((wave_gemm<Sh, OP, TA, TB, false>), dim3(unsigned(p.whole_tiles)), dim3(256), 0, s, p);
+  }
+  if(p.split.tiles) {
+    hipLaunchKernelGGL((wave_split<Sh, OP, TA, TB>), dim3(unsigned(p.split.xcds * p.split.units)), dim3(256), 0, s, p);
+    if(const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    return launch_fixup<Sh, INT>(p, s);
+  }
   return hipGetLastError();
 }
 

@@ -17,8 +17,8 @@ LIBRARY = HERE / "libcairn_gemm_gfx950.so"
 # enum cairn_type, cairn_act, cairn_status
 F32, F16, BF16, F8E4M3, F8E5M2, I8, I32 = range(7)
 ACT_NONE, ACT_RELU, ACT_GELU = range(3)
-OK, E_SHAPE, E_TYPE, E_KERNEL, E_ARG, E_HIP = range(6)
-DESC_VERSION = 1
+OK, E_SHAPE, E_TYPE, E_KERNEL, E_ARG, E_HIP, E_SCRATCH = range(7)
+DESC_VERSION = 2
 # enum cairn_scale_mode, cairn_quant_status
 SCALE_ROW_ABSMAX, SCALE_ROW, SCALE_TENSOR = range(3)
 QUANT_BAD_SCALE, QUANT_NAN = 1, 2
@@ -62,6 +62,9 @@ class Desc(C.Structure):
         ("row_scale", C.c_void_p),
         ("col_scale", C.c_void_p),
         ("kernel", C.c_int32),
+        ("workspace", C.c_void_p),
+        ("workspace_bytes", C.c_uint64),
+        ("split_units", C.c_int32),
     ]
 
 
@@ -114,6 +117,9 @@ class Choice(C.Structure):
         ("workgroups", C.c_uint64),
         ("waves", C.c_double),
         ("efficiency", C.c_double),
+        ("split_tiles", C.c_int32),
+        ("split_units", C.c_int32),
+        ("split_bytes", C.c_uint64),
     ]
 
 
@@ -123,6 +129,7 @@ _MMA = [SZ, SZ, SZ, SZ, C.c_void_p, SZ, C.c_void_p, SZ, C.c_void_p]
 SIGNATURES = {
     "cairn_gemm_run": (C.c_int, [C.POINTER(Desc), C.c_void_p]),
     "cairn_gemm_select": (C.c_int, [C.POINTER(Desc), C.POINTER(Choice)]),
+    "cairn_gemm_workspace": (C.c_int, [C.POINTER(Desc), C.POINTER(C.c_uint64)]),
     "cairn_gemm_kernel_count": (C.c_int, []),
     "cairn_gemm_kernel_info": (C.c_int, [C.c_int32, C.POINTER(Kernel)]),
     "cairn_gemm_status_string": (C.c_char_p, [C.c_int]),
@@ -160,10 +167,20 @@ def status_string(status: int) -> str:
 def desc(ab_type: int, c_type: int, m: int, n: int, k: int, a=None, b=None, c=None, *, trans_a: bool = False,
          trans_b: bool = False, lda: int = 0, ldb: int = 0, ldc: int = 0, accumulate: bool = False,
          act: int = ACT_NONE, bias=None, bias_type: int = F32, row_scale=None, col_scale=None,
-         kernel: int = 0) -> Desc:  # fmt: skip
+         kernel: int = 0, workspace=None, workspace_bytes: int = 0, split_units: int = 0) -> Desc:  # fmt: skip
     """A cairn_gemm_desc; pointers are ints (device addresses) or None."""
     return Desc(DESC_VERSION, ab_type, c_type, int(trans_a), int(trans_b), m, n, k, lda, ldb, ldc, a, b, c,
-                int(accumulate), act, bias, bias_type, row_scale, col_scale, kernel)  # fmt: skip
+                int(accumulate), act, bias, bias_type, row_scale, col_scale, kernel, workspace, workspace_bytes,
+                split_units)  # fmt: skip
+
+
+def workspace(d: Desc) -> int:
+    """The bytes a split last round of `d` would use (cairn_gemm_workspace)."""
+    out = C.c_uint64(0)
+    s = load().cairn_gemm_workspace(C.byref(d), C.byref(out))
+    if s != OK:
+        raise GemmError(s, status_string(s))
+    return out.value
 
 
 def run(d: Desc, stream: int | None = None) -> None:
@@ -192,7 +209,8 @@ def select(d: Desc) -> dict:
     info = kernel_info(choice.kernel)
     return {"kernel": choice.kernel, "name": info["name"], "family": FAMILY[choice.family], "tile_m": choice.tile_m,
             "tile_n": choice.tile_n, "tile_k": choice.tile_k, "workgroups": choice.workgroups,
-            "waves": choice.waves, "efficiency": choice.efficiency}  # fmt: skip
+            "waves": choice.waves, "efficiency": choice.efficiency, "split_tiles": choice.split_tiles,
+            "split_units": choice.split_units, "split_bytes": choice.split_bytes}  # fmt: skip
 
 
 def kernel_info(kid: int) -> dict:

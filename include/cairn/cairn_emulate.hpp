@@ -111,7 +111,7 @@ struct Emulated {
   // A descriptor's GEMM on the host: for each output its products in increasing p (f32, or exact int32 for int8),
   // then the epilogue's steps, each an f32 rounding, in the order cairn_gemm.h states, and the output's rounding.
   void gemm(const cairn_gemm_desc& d, Stream) noexcept {
-    if(d.version != CAIRN_GEMM_DESC_VERSION) trap();
+    if(d.version != 1u && d.version != CAIRN_GEMM_DESC_VERSION) trap();
     const std::size_t lda = d.lda ? d.lda : (d.trans_a ? d.m : d.k), ldb = d.ldb ? d.ldb : (d.trans_b ? d.k : d.n);
     const std::size_t ldc = d.ldc ? d.ldc : d.n;
     for(std::size_t i = 0; i < d.m; ++i)

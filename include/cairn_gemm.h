@@ -57,10 +57,11 @@ enum cairn_status {
   CAIRN_E_TYPE = 2,    /* an operand/output/bias type combination no kernel computes */
   CAIRN_E_KERNEL = 3,  /* the kernel id named does not exist or cannot run this problem */
   CAIRN_E_ARG = 4,     /* a null pointer where data is needed, or a bad descriptor version */
-  CAIRN_E_HIP = 5      /* the HIP runtime refused the launch */
+  CAIRN_E_HIP = 5,     /* the HIP runtime refused the launch */
+  CAIRN_E_SCRATCH = 6  /* the split last round asked for needs more scratch than the workspace given holds */
 };
 
-#define CAIRN_GEMM_DESC_VERSION 1u
+#define CAIRN_GEMM_DESC_VERSION 2u /* version 1: the descriptor up to `kernel`, with no split */
 
 /*
  * One GEMM: c = epilogue(a * b). a is m x k, stored row-major (trans_a = 0) or as its transpose, k x m row-major
@@ -93,6 +94,16 @@ typedef struct cairn_gemm_desc {
   const float* row_scale;
   const float* col_scale;
   int32_t kernel; /* 0: the selector's choice; else an id cairn_gemm_kernel_info knows */
+  /* The split last round (version 2). Where the output tiles are not a whole number of rounds of the machine's 256
+   * CUs, the tiles of the last, partial round can be shared along k by `split_units` workgroups, each adding its
+   * share into partial tiles in `workspace`; a fixup pass adds each tile's partials in k order (so the result's bits
+   * do not depend on timing) and applies the epilogue. cairn_gemm_workspace says how many bytes the split needs.
+   * workspace NULL, or split_units -1: no split. split_units 0: the selector's choice (where it pays, and within
+   * workspace_bytes). The workspace is the caller's device memory, 256-byte aligned, not shared with a call that
+   * may run at the same time. */
+  void* workspace;
+  uint64_t workspace_bytes;
+  int32_t split_units;
 } cairn_gemm_desc;
 
 /* A kernel of the library: its id, what it computes and the tile it runs. */
@@ -116,6 +127,9 @@ typedef struct cairn_gemm_choice {
   uint64_t workgroups;   /* launched */
   double waves;          /* workgroups / (CUs x workgroups resident per CU) */
   double efficiency;     /* the share of the machine the tiling keeps busy: whole-wave and edge-tile losses */
+  int32_t split_tiles;   /* tiles of the split last round (0: none) */
+  int32_t split_units;   /* workgroups sharing them along k */
+  uint64_t split_bytes;  /* the workspace they use */
 } cairn_gemm_choice;
 
 /* Queue the GEMM on `stream`. Returns without waiting, allocates nothing and makes no stream or event, so it may be
@@ -124,6 +138,10 @@ int cairn_gemm_run(const cairn_gemm_desc* d, void* stream);
 
 /* The kernel cairn_gemm_run would launch for `d` (d->kernel 0) or checks that d->kernel can run it. No GPU call. */
 int cairn_gemm_select(const cairn_gemm_desc* d, cairn_gemm_choice* out);
+
+/* The workspace bytes a split last round of `d` would use with unlimited room (0 where the selector would not split
+ * it, or d->split_units is -1): what a caller allocates for d->workspace. No GPU call. */
+int cairn_gemm_workspace(const cairn_gemm_desc* d, uint64_t* bytes);
 
 /* The kernel table: count, and the entry for one id (1 .. count). */
 int cairn_gemm_kernel_count(void);
@@ -221,7 +239,7 @@ int cairn_quantize_run(const cairn_quantize_desc* d, void* stream);
  * the build refuses a header whose identity is stale. A translation unit that uses the header's types without the
  * library (a host-only test machine, or an emulated build: CAIRN_EMULATE) defines CAIRN_GEMM_UNLINKED.
  */
-#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_41cf1b6ef10665c0
+#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_46c2aceb567fe8a8
 extern const char CAIRN_GEMM_IDENTITY[];
 #if !defined(CAIRN_GEMM_UNLINKED) && !defined(CAIRN_EMULATE)
 static const char* const cairn_interface_of_gemm_gfx950 __attribute__((used)) = CAIRN_GEMM_IDENTITY;

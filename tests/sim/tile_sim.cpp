@@ -581,6 +581,69 @@ int main() {
             return 1;
           }
       }
+  // The split last round, per XCD block: every (tile, stage) in exactly one unit's segment, every slot used once over
+  // all XCDs, each tile's units (split_units_of) naming its segments in k order with the slots they were written to
+  // (split_slot), and the whole-tile pass and the split tiles together covering every id once.
+  for(int xcds : {1, 8})
+    for(int tiles = 1; tiles <= 31; tiles += (tiles < 16 ? 1 : 5))
+      for(int stages : {1, 2, 3, 4, 7, 16, 64, 65, 128})
+        for(int units : {1, 7, 16, 31, 32}) {
+          const long long total = (long long)tiles * stages;
+          const int quota = int((total + units - 1) / units);
+          if(quota > stages) continue;  // the planner never asks for this
+          const int first = 64, block = first + tiles;
+          Split s{first, tiles, stages, quota, int((total + quota - 1) / quota), xcds, block};
+          std::vector<int> slot_used(2 * xcds * s.units, 0), id_seen(xcds * block, 0);
+          for(int b = 0; b < xcds * first; ++b) ++id_seen[whole_id(s, b)];
+          for(int x = 0; x < xcds; ++x) {
+            std::vector<int> owner(total, -1);
+            for(int v = 0; v < s.units; ++v)
+              for(int j = 0; j < 2; ++j) {
+                int tile, s0, s1;
+                if(!split_segment(s, v, j, tile, s0, s1)) continue;
+                const int slot = 2 * (v * xcds + x) + j;  // what workgroup u = v xcds + x writes
+                if(tile < 0 || tile >= tiles || s0 < 0 || s1 > stages || s0 >= s1 || slot_used[slot]++) {
+                  std::printf("split segment off its tile, or a slot written twice\n");
+                  return 1;
+                }
+                for(int st = s0; st < s1; ++st) {
+                  if(owner[(long long)tile * stages + st] != -1) {
+                    std::printf("split stage run twice\n");
+                    return 1;
+                  }
+                  owner[(long long)tile * stages + st] = slot;
+                }
+              }
+            for(int o : owner)
+              if(o < 0) {
+                std::printf("split stage never run (%d tiles, %d stages, %d units)\n", tiles, stages, units);
+                return 1;
+              }
+            for(int tl = 0; tl < tiles; ++tl) {
+              ++id_seen[split_id(s, x, tl)];
+              int lo, hi;
+              split_units_of(s, tl, lo, hi);
+              int next = 0;  // the tile's next stage in k order
+              for(int v = lo; v <= hi; ++v) {
+                const int slot = split_slot(s, x, tl, v);
+                if(owner[(long long)tl * stages + next] != slot) {
+                  std::printf("split fixup reads the wrong slot\n");
+                  return 1;
+                }
+                while(next < stages && owner[(long long)tl * stages + next] == slot) ++next;
+              }
+              if(next != stages) {
+                std::printf("split fixup misses stages of a tile\n");
+                return 1;
+              }
+            }
+          }
+          for(int seen : id_seen)
+            if(seen != 1) {
+              std::printf("the two passes do not cover every tile id once\n");
+              return 1;
+            }
+        }
   if(failures) return 1;
   std::printf("ok: every tile equals the exact product\n");
   return 0;

@@ -214,7 +214,7 @@ def test_the_selector_refuses_what_no_kernel_computes():
     assert status(c=None) == L.E_ARG
     assert status(act=7) == L.E_ARG
     bad = L.desc(L.BF16, L.F32, 64, 64, 64, P, P, P)
-    bad.version = 2
+    bad.version = 3  # no such version
     assert L.load().cairn_gemm_select(C.byref(bad), None) == L.E_ARG
     assert status(m=0, c=None) == L.OK  # nothing to do needs no pointers
 
@@ -252,3 +252,55 @@ except L.LibraryMissing as e:
 """
     done = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert "missing:" in done.stdout, done.stdout + done.stderr
+
+
+def test_the_selector_splits_a_nearly_idle_last_round_where_a_workspace_is_given():
+    """264 tiles of k = 8192 (one round and one tile an XCD): with the workspace cairn_gemm_workspace asks for, the
+    last round's 8 tiles are shared along k by 4 units an XCD (no unit below 8 stages) and the tiling keeps the
+    machine >= 97% busy; without a workspace it runs whole. C3's rounds (5.375 and 2.69: a quarter or more of the CUs
+    busy in the last one) and C2 (one whole round) are not split by the selector: measured, a split round there was
+    slower than the whole one (the clock rises when CUs idle)."""
+    P = 1 << 20
+    plain = L.desc(L.BF16, L.BF16, 2048, 8448, 8192, P, P, P)
+    assert L.select(plain)["split_tiles"] == 0 and L.select(plain)["efficiency"] < 0.6
+    need = L.workspace(plain)
+    assert need == 2 * 8 * 32 * 256 * 256 * 4  # two partial tiles a unit, 32 units an XCD (256 stages / 8)
+    given = L.desc(L.BF16, L.BF16, 2048, 8448, 8192, P, P, P, workspace=P, workspace_bytes=need)
+    ch = L.select(given)
+    assert ch["split_tiles"] == 8 and ch["split_units"] == 256 and ch["efficiency"] >= 0.97, ch
+    for m, n, k, ta in ((8192, 11008, 4096, False), (4096, 11008, 8192, True), (4096, 4096, 4096, False)):
+        d = L.desc(L.BF16, L.BF16, m, n, k, P, P, P, trans_a=ta, workspace=P, workspace_bytes=1 << 30)
+        assert L.workspace(d) == 0 and L.select(d)["split_tiles"] == 0, (m, n, k)
+    # Asked for explicitly, the MLP forward's last round splits over 256 units.
+    fwd = L.desc(L.BF16, L.BF16, 8192, 11008, 4096, P, P, P, workspace=P, workspace_bytes=1 << 30, split_units=256)
+    ch = L.select(fwd)
+    assert ch["split_tiles"] == 96 and ch["split_units"] == 256 and ch["efficiency"] >= 0.97, ch
+
+
+def test_an_explicit_split_is_checked_against_its_workspace():
+    P = 1 << 20
+    lib = L.load()
+
+    def status(**kw):
+        d = L.desc(L.BF16, L.BF16, 2048, 8448, 1024, P, P, P, **kw)
+        return lib.cairn_gemm_select(C.byref(d), None)
+
+    assert status(split_units=64) == L.E_SCRATCH  # no workspace at all
+    assert status(split_units=64, workspace=P, workspace_bytes=64 * 2 * 256 * 1024) == L.OK
+    assert status(split_units=64, workspace=P, workspace_bytes=64 * 2 * 256 * 1024 - 1) == L.E_SCRATCH
+    # 272 tiles: 8 XCD blocks of 34, each splitting 2; one unit an XCD would span both tiles and more.
+    d = L.desc(L.BF16, L.BF16, 2048, 8704, 1024, P, P, P, workspace=P, workspace_bytes=1 << 30, split_units=8)
+    assert lib.cairn_gemm_select(C.byref(d), None) == L.E_ARG
+    assert status(split_units=-2) == L.E_ARG
+    assert status(workspace=P + 16, workspace_bytes=1 << 30) == L.E_ARG  # off 256 bytes
+    # A version 1 descriptor (up to `kernel`) is read as such and never splits.
+    old = L.desc(L.BF16, L.BF16, 8192, 11008, 4096, P, P, P, workspace=P, workspace_bytes=1 << 30)
+    old.version = 1
+    choice = L.Choice()
+    assert lib.cairn_gemm_select(C.byref(old), C.byref(choice)) == L.OK and choice.split_tiles == 0
+
+
+def test_the_bindings_use_the_headers_descriptor_versions():
+    text = HEADER.read_text()
+    assert int(re.search(r"#define CAIRN_GEMM_DESC_VERSION (\d+)u", text).group(1)) == L.DESC_VERSION
+    assert int(re.search(r"#define CAIRN_QUANTIZE_DESC_VERSION (\d+)u", text).group(1)) == L.QUANTIZE_DESC_VERSION

@@ -6,6 +6,7 @@ cannot see into; this test reads what the compiler emitted and holds it to that.
 
 from __future__ import annotations
 
+import concurrent.futures
 import re
 import shutil
 import subprocess
@@ -23,17 +24,19 @@ def assembly(tmp_path_factory) -> str:
     if not shutil.which("hipcc"):
         pytest.skip("hipcc is not installed")
     where = tmp_path_factory.mktemp("isa")
-    texts = []
-    for src in sorted((ROOT / "cairn_amd" / "csrc").glob("gemm_wave_*.hip")):
+
+    def compiled(src: Path) -> str:
         out = where / (src.stem + ".s")
-        subprocess.run(["hipcc", *FLAGS, str(src), "-o", str(out)], check=True, capture_output=True, timeout=600)
-        texts.append(out.read_text())
-    return "\n".join(texts)
+        subprocess.run(["hipcc", *FLAGS, str(src), "-o", str(out)], check=True, capture_output=True, timeout=900)
+        return out.read_text()
+
+    with concurrent.futures.ThreadPoolExecutor(4) as pool:
+        return "\n".join(pool.map(compiled, sorted((ROOT / "cairn_amd" / "csrc").glob("gemm_wave_*.hip"))))
 
 
 def kernels(asm: str) -> dict[str, list[str]]:
     found = {}
-    for m in re.finditer(r"^(_ZN5cairn4gemm(?:9wave_gemm|10wave8_gemm)\S*):", asm, re.M):
+    for m in re.finditer(r"^(_ZN5cairn4gemm(?:9wave_gemm|10wave8_gemm|10wave_split|11wave8_split)\S*):", asm, re.M):
         body = asm[m.end():asm.index(".Lfunc_end", m.end())]
         found[m.group(1)] = [line.split(";")[0].strip() for line in body.splitlines() if line.strip()]
     return found
@@ -41,7 +44,7 @@ def kernels(asm: str) -> dict[str, list[str]]:
 
 def test_every_lds_load_group_starts_with_its_own_base(assembly):
     ks = kernels(assembly)
-    assert len(ks) >= 20
+    assert len(ks) >= 40  # the whole-tile and split kernels of every instance
     for name, lines in ks.items():
         groups, current = [], None
         for line in lines:
@@ -69,7 +72,7 @@ def test_the_main_loop_writes_m0_twice_per_stage(assembly):
                     loops.append(lines[start:i])
         assert loops, name
         loop = max(loops, key=lambda seg: sum(x.startswith("v_mfma") for x in seg))  # the main loop
-        fp8 = "wave8_gemm" in name  # one 32x32x64 MFMA a block and stage; the int8 layout's two k-steps otherwise
+        fp8 = "wave8_" in name  # one 32x32x64 MFMA a block and stage; the int8 layout's two k-steps otherwise
         mfmas = sum(x.startswith("v_mfma") for x in loop)
         stages = mfmas // (16 if fp8 else 32)
         # Every steady loop is unrolled by the ring's four stages.
@@ -110,5 +113,5 @@ def test_the_steady_loop_issues_in_the_mfmas_shadow(assembly):
                 if start < i and any("s_barrier" in x for x in lines[start:i]):
                     loops.append(lines[start:i + 1])
         loop = max(loops, key=lambda seg: sum(x.startswith("v_mfma") for x in seg))
-        cycles, ideal = issue_cycles(loop, 64 if "wave8_gemm" in name else 32)
+        cycles, ideal = issue_cycles(loop, 64 if "wave8_" in name else 32)
         assert cycles <= 1.01 * ideal, (name, cycles, ideal)
