@@ -23,6 +23,7 @@ DESC_VERSION = 2
 SCALE_ROW_ABSMAX, SCALE_ROW, SCALE_TENSOR = range(3)
 QUANT_BAD_SCALE, QUANT_NAN = 1, 2
 QUANTIZE_DESC_VERSION = 1
+STATIC_SCRATCH = 64 << 20  # CAIRN_GEMM_STATIC_SCRATCH
 FAMILY = {0: "mfma", 1: "generic", 2: "skinny", 4: "wave"}
 TYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", F8E4M3: "f8e4m3", F8E5M2: "f8e5m2", I8: "i8", I32: "i32"}
 
@@ -128,6 +129,7 @@ SZ = C.c_size_t
 _MMA = [SZ, SZ, SZ, SZ, C.c_void_p, SZ, C.c_void_p, SZ, C.c_void_p]
 SIGNATURES = {
     "cairn_gemm_run": (C.c_int, [C.POINTER(Desc), C.c_void_p]),
+    "cairn_gemm_run_static": (C.c_int, [C.POINTER(Desc), C.c_void_p]),
     "cairn_gemm_select": (C.c_int, [C.POINTER(Desc), C.POINTER(Choice)]),
     "cairn_gemm_workspace": (C.c_int, [C.POINTER(Desc), C.POINTER(C.c_uint64)]),
     "cairn_gemm_kernel_count": (C.c_int, []),

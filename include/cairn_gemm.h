@@ -136,6 +136,16 @@ typedef struct cairn_gemm_choice {
  * captured in a HIP graph. A nonzero status means nothing was queued (CAIRN_E_HIP: the launch itself failed). */
 int cairn_gemm_run(const cairn_gemm_desc* d, void* stream);
 
+/* cairn_gemm_run for callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). It has no counterpart in the reference. The split last round's workspace is a scratch array the library
+ * holds on each GPU (CAIRN_GEMM_STATIC_SCRATCH bytes, from the library's load to the process's end); d->workspace must
+ * be NULL (else CAIRN_E_ARG). The selector's split fits the scratch; a split asked for (d->split_units > 0) that needs
+ * more answers CAIRN_E_SCRATCH and queues nothing. It allocates nothing, frees nothing and makes no stream or event.
+ * Every call on one GPU shares that GPU's scratch and leaves its contents to the next: two calls that may run at the
+ * same time on one GPU (two streams, two threads) race on it. */
+#define CAIRN_GEMM_STATIC_SCRATCH (64u << 20)
+int cairn_gemm_run_static(const cairn_gemm_desc* d, void* stream);
+
 /* The kernel cairn_gemm_run would launch for `d` (d->kernel 0) or checks that d->kernel can run it. No GPU call. */
 int cairn_gemm_select(const cairn_gemm_desc* d, cairn_gemm_choice* out);
 
@@ -239,7 +249,7 @@ int cairn_quantize_run(const cairn_quantize_desc* d, void* stream);
  * the build refuses a header whose identity is stale. A translation unit that uses the header's types without the
  * library (a host-only test machine, or an emulated build: CAIRN_EMULATE) defines CAIRN_GEMM_UNLINKED.
  */
-#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_46c2aceb567fe8a8
+#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_5e01d71c3bad89c7
 extern const char CAIRN_GEMM_IDENTITY[];
 #if !defined(CAIRN_GEMM_UNLINKED) && !defined(CAIRN_EMULATE)
 static const char* const cairn_interface_of_gemm_gfx950 __attribute__((used)) = CAIRN_GEMM_IDENTITY;
