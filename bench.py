@@ -51,9 +51,11 @@ def bf16(x: np.ndarray) -> np.ndarray:
     return ((u + np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1))) >> 16).astype(np.uint16)
 
 
-def timed(descs: list, stream: hip.Stream, steps: int, warmup: int, launch=L.run) -> dict:
-    """Warm-up, then `steps` launches cycling through `descs` between two synchronizations: wall time per step and
-    the events' average kernel time on the stream."""
+def timed(descs: list, stream: hip.Stream, steps: int, warmup: int, launch=L.run, reps: int = 50) -> dict:
+    """Warm-up, then two measurements of launches cycling through `descs`:
+    - the burst: `steps` launches back to back between two synchronizations, timed by the wall clock and by an event
+      pair around them on the stream (the average launch of a full queue);
+    - the reps: `reps` launches, each between an event pair of its own on the stream: the median and the fastest."""
     for i in range(warmup):
         launch(descs[i % len(descs)], stream.handle)
     stream.synchronize()
@@ -70,7 +72,18 @@ def timed(descs: list, stream: hip.Stream, steps: int, warmup: int, launch=L.run
     gpu_ms = start.elapsed_ms(end)
     start.close()
     end.close()
-    return {"wall_ms_per_step": wall * 1e3 / steps, "event_ms_per_step": gpu_ms / steps}
+    pairs = [(hip.Event(), hip.Event()) for _ in range(reps)]
+    for i, (a, b) in enumerate(pairs):
+        a.record(stream)
+        launch(descs[i % len(descs)], stream.handle)
+        b.record(stream)
+    stream.synchronize()
+    each = sorted(a.elapsed_ms(b) for a, b in pairs)
+    for a, b in pairs:
+        a.close()
+        b.close()
+    return {"wall_ms_per_step": wall * 1e3 / steps, "event_ms_per_step": gpu_ms / steps,
+            "median_ms": each[len(each) // 2], "min_ms": each[0], "reps": reps}  # fmt: skip
 
 
 def square(ab: int, out: int, n: int, rng, **kw) -> tuple[L.Desc, list]:
@@ -103,7 +116,8 @@ def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict
     log("bf16 4096^3 on", choice["name"])
     t = timed([d], stream, steps, warmup)
     bf = {"kernel": choice["name"], "tflops": flops / (t["wall_ms_per_step"] * 1e-3) / 1e12,
-          "kernel_tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12, **t}  # fmt: skip
+          "kernel_tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
+          "median_tflops": flops / (t["median_ms"] * 1e-3) / 1e12, **t}  # fmt: skip
     for x in bufs:
         x.close()
     d, bufs = square(L.I8, L.BF16, n, rng, row_scale=True)
@@ -112,7 +126,8 @@ def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict
     log("int8 4096^3 on", choice["name"])
     t = timed([d], stream, steps, warmup)
     i8 = {"kernel": choice["name"], "tops": flops / (t["wall_ms_per_step"] * 1e-3) / 1e12,
-          "kernel_tops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12, **t}  # fmt: skip
+          "kernel_tops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
+          "median_tops": flops / (t["median_ms"] * 1e-3) / 1e12, **t}  # fmt: skip
     i8["frac"] = i8["kernel_tops"] / PEAK_I8
     for x in bufs:
         x.close()
@@ -126,7 +141,8 @@ def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict
     log("f8e4m3 4096^3 on", choice["name"])
     t = timed([d], stream, steps, warmup)
     f8 = {"kernel": choice["name"], "tflops": flops / (t["wall_ms_per_step"] * 1e-3) / 1e12,
-          "kernel_tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12, **t}  # fmt: skip
+          "kernel_tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
+          "median_tflops": flops / (t["median_ms"] * 1e-3) / 1e12, **t}  # fmt: skip
     f8["frac"] = f8["kernel_tflops"] / PEAK_FP8
     for x in bufs:
         x.close()
@@ -148,7 +164,8 @@ def bench_skinny(stream, steps, warmup) -> dict:
         moved = 2.0 * (m * k + n * k + m * n)
         out[f"m{m}"] = {"kernel": choice["name"], "bytes": int(moved),
                         "gbps": moved / (t["event_ms_per_step"] * 1e-3) / 1e9,
-                        "frac": moved / (t["event_ms_per_step"] * 1e-3) / 1e9 / PEAK_HBM, **t}  # fmt: skip
+                        "frac": moved / (t["event_ms_per_step"] * 1e-3) / 1e9 / PEAK_HBM,
+                        "median_gbps": moved / (t["median_ms"] * 1e-3) / 1e9, **t}  # fmt: skip
         log(f"skinny m={m}: {out[f'm{m}']['gbps']:.0f} GB/s on {choice['name']}")
         a.close()
         c.close()
@@ -167,14 +184,15 @@ def bench_quantize(stream, steps, warmup) -> dict:
     qs = [hip.Buffer(m * k) for _ in range(copies)]
     ss = [hip.Buffer(m * 4) for _ in range(copies)]
     descs = [L.quantize_desc(L.BF16, L.I8, m, k, x.ptr, q.ptr, s.ptr) for x, q, s in zip(xs, qs, ss)]
+    kernel = L.quantize_kernel(descs[0])
     t = timed(descs, stream, max(steps, 4 * copies), warmup, launch=L.quantize)
     moved = m * k * 2 + m * k + m * 4
     gbps = moved / (t["event_ms_per_step"] * 1e-3) / 1e9
-    log(f"quantize bf16->int8 {m}x{k}: {gbps:.0f} GB/s")
+    log(f"quantize bf16->int8 {m}x{k}: {gbps:.0f} GB/s on {kernel}")
     for b in (*xs, *qs, *ss):
         b.close()
-    return {"metric": "bf16 -> int8 per-row quantize 8192x4096, HBM GB/s", "kernel": "quantize_rows<bf16, i8>",
-            "bytes": moved, "gbps": gbps, "frac": gbps / PEAK_HBM, **t}  # fmt: skip
+    return {"metric": "bf16 -> int8 per-row quantize 8192x4096, HBM GB/s", "kernel": kernel, "bytes": moved,
+            "gbps": gbps, "frac": gbps / PEAK_HBM, "median_gbps": moved / (t["median_ms"] * 1e-3) / 1e9, **t}  # fmt: skip
 
 
 def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
@@ -208,6 +226,7 @@ def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
         out[name] = {"kernel": ch["name"], "tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
                      "split_tiles": ch["split_tiles"], "split_units": ch["split_units"],
                      "efficiency": round(ch["efficiency"], 4),
+                     "median_tflops": flops / (t["median_ms"] * 1e-3) / 1e12,
                      "tflops_whole_rounds": flops / (tw["event_ms_per_step"] * 1e-3) / 1e12, **t}  # fmt: skip
         log(f"mlp {name}: {out[name]['tflops']:.0f} TFLOP/s on {ch['name']} (split {ch['split_tiles']} tiles; "
             f"whole rounds {out[name]['tflops_whole_rounds']:.0f})")  # fmt: skip
@@ -293,37 +312,119 @@ def bench_calibrate(stream, steps: int, warmup: int) -> dict:
 COPY_BYTES = 1 << 30
 
 
-def bench_traffic(stream, launches: int = 3, family: str | None = None) -> dict:
-    """The program the two counter passes profile (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): `launches` launches
-    of the dominant kernel on the bench's own 4096^3 bf16 problem, then `launches` device-to-device copies of
-    COPY_BYTES, whose counter readings against their known bytes (COPY_BYTES read, COPY_BYTES written) give the
-    scale from the counters' KiB to bytes moved."""
+def bench_counters(stream, launches: int = 3) -> dict:
+    """The program the counter passes profile (rocprofv3 --pmc, one pass a counter set): `launches` launches of each
+    workload below, in this order, then `launches` device-to-device copies of COPY_BYTES (their readings against
+    the bytes they move scale the memory counters). Returns the order, which the summaries label dispatches by.
+    - C2: bf16 4096^3 NN, bf16 out;
+    - C4: int8 W8A8 4096^3, dequant to bf16;
+    - C3: the MLP layer's forward (8192 x 11008 x 4096 NN, bias + GELU), dX (NT) and dW (TN);
+    - C5: the decode GEMMs m = 1, 4, 16 (n = 14336, k = 4096, b stored n x k), each launch on another of 4 copies of
+      b (4 x 117 MB, past the 256 MB MALL)."""
     rng = np.random.default_rng(20261201)
-    d, bufs = square(L.BF16, L.BF16, 4096, rng)
-    if family:
-        d.kernel = L.kernel_named(f"cairn_{family}_bf16_nn_256x256")
-    name = L.select(d)["name"]
-    for _ in range(launches):
-        L.run(d, stream.handle)
-    stream.synchronize()
+    order, keep = [], []
+    d2, b2 = square(L.BF16, L.BF16, 4096, rng)
+    d4, b4 = square(L.I8, L.BF16, 4096, rng, row_scale=True)
+    keep += b2 + b4
+    M, K, N = 8192, 4096, 11008
+    x = hip.Buffer.of(bf16(rng.normal(0, 0.02, (M, K)).astype(np.float32)))
+    w = hip.Buffer.of(bf16(rng.normal(0, 0.02, (K, N)).astype(np.float32)))
+    bias = hip.Buffer.of(bf16(rng.normal(0, 0.02, (N,)).astype(np.float32)))
+    dy = hip.Buffer.of(bf16(rng.standard_normal((M, N), dtype=np.float32)))
+    y, dx, dw = hip.Buffer(M * N * 2), hip.Buffer(M * K * 2), hip.Buffer(K * N * 2)
+    keep += [x, w, bias, dy, y, dx, dw]
+    fwd = L.desc(L.BF16, L.BF16, M, N, K, x.ptr, w.ptr, y.ptr, bias=bias.ptr, bias_type=L.BF16, act=L.ACT_GELU)
+    bwd_x = L.desc(L.BF16, L.BF16, M, K, N, dy.ptr, w.ptr, dx.ptr, trans_b=True)
+    bwd_w = L.desc(L.BF16, L.BF16, K, N, M, x.ptr, dy.ptr, dw.ptr, trans_a=True)
+    n, k = 14336, 4096
+    bs = [hip.Buffer.of(bf16(rng.standard_normal((n, k), dtype=np.float32) / np.float32(64.0))) for _ in range(4)]
+    keep += bs
+    work = [("C2 bf16 4096^3 NN", [d2]), ("C4 int8 W8A8 4096^3", [d4]), ("C3 forward NN + bias + GELU", [fwd]),
+            ("C3 dX NT", [bwd_x]), ("C3 dW TN", [bwd_w])]  # fmt: skip
+    for m in (1, 4, 16):
+        a = hip.Buffer.of(bf16(rng.standard_normal((m, k), dtype=np.float32)))
+        c = hip.Buffer(m * n * 2)
+        keep += [a, c]
+        work.append((f"C5 decode m={m}", [L.desc(L.BF16, L.BF16, m, n, k, a.ptr, b.ptr, c.ptr, trans_b=True) for b in bs]))
+    for name, descs in work:
+        kernel = L.select(descs[0])["name"]
+        for i in range(launches):
+            L.run(descs[i % len(descs)], stream.handle)
+        stream.synchronize()
+        order.append({"workload": name, "kernel": kernel, "launches": launches})
     src, dst = hip.Buffer(COPY_BYTES), hip.Buffer(COPY_BYTES)
     src.zero()
     hip.synchronize()
     for _ in range(launches):
         dst.copy_from(src)
     hip.synchronize()
-    for b in (*bufs, src, dst):
+    order.append({"workload": f"copy of {COPY_BYTES} bytes", "kernel": "(runtime copy)", "launches": launches})
+    for b in (*keep, src, dst):
         b.close()
-    return {"kernel": name, "launches": launches, "copy_bytes": COPY_BYTES}
+    return {"order": order, "copy_bytes": COPY_BYTES}
 
 
-TRAFFIC = ROOT / "profiles" / "traffic_wave_bf16_4096.md"
+CEILING = ROOT / "tests" / "cpp" / "libmfma_ceiling.so"
+
+
+def bench_ceiling(stream, steps: int, warmup: int, iterations: int = 8192) -> dict:
+    """The MFMA-only ceiling (tests/cpp/mfma_ceiling.hip): one workgroup a CU, its four waves issuing independent
+    MFMAs on register operands of random data of each type, with no memory traffic. The rate comes from the
+    launches' events; each CU's clock and the cycles an MFMA took, from the last launch's stamps."""
+    if not CEILING.exists():
+        raise SystemExit(f"{CEILING} is not built: run __graft_entry__.build()")
+    lib = C.CDLL(str(CEILING))
+    lib.ceiling_launch.restype = C.c_int
+    lib.ceiling_launch.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    lib.ceiling_flop_per_mfma.restype, lib.ceiling_flop_per_mfma.argtypes = C.c_long, [C.c_int]
+    chains, khz = lib.ceiling_chains(), lib.ceiling_wall_khz()
+    cus = hip.describe(0).get("cus", 256)
+    rng = np.random.default_rng(4)
+    count = 4096  # 16-byte patterns
+    e4m3 = rng.integers(0, 256, count * 16, dtype=np.uint8)
+    e4m3[(e4m3 & 0x7F) == 0x7F] &= 0xBF  # finite patterns only
+    patterns = {
+        "bf16": (0, PEAK_BF16, bf16(rng.standard_normal(count * 8, dtype=np.float32)).view(np.uint8)),
+        "i8": (1, PEAK_I8, rng.integers(-127, 128, count * 16, dtype=np.int8).view(np.uint8)),
+        "f8e4m3": (2, PEAK_FP8, e4m3),
+    }
+    out, stamps = hip.Buffer(cus * 256 * 4), hip.Buffer(cus * 4 * 8)
+    result = {"workgroups": cus, "waves_per_workgroup": 4, "chains": chains, "iterations": iterations,
+              "wall_clock_khz": khz}  # fmt: skip
+    for name, (kind, peak, pats) in patterns.items():
+        ops = hip.Buffer.of(pats)
+
+        def launch(_, handle, kind=kind, ops=ops):
+            e = lib.ceiling_launch(kind, cus, iterations, ops.ptr, count, out.ptr, stamps.ptr, handle)
+            if e != 0:
+                raise RuntimeError(f"ceiling_launch: hipError {e}")
+
+        t = timed([None], stream, steps, warmup, launch=launch)
+        st = stamps.download((cus, 4), np.uint64).astype(np.float64)
+        cycles = st[:, 1] - st[:, 0]
+        mhz = cycles / ((st[:, 3] - st[:, 2]) / (khz * 1e3)) / 1e6 if khz else np.zeros(1)
+        flop = cus * 4 * chains * iterations * lib.ceiling_flop_per_mfma(kind)
+        rate = flop / (t["event_ms_per_step"] * 1e-3) / 1e12
+        result[name] = {"tflops": rate, "frac": rate / peak, "median_tflops": flop / (t["median_ms"] * 1e-3) / 1e12,
+                        "cycles_per_mfma": float(np.median(cycles)) / (chains * iterations),
+                        "clock_mhz": {"min": float(mhz.min()), "median": float(np.median(mhz)), "max": float(mhz.max())},
+                        **t}  # fmt: skip
+        log(f"ceiling {name}: {rate:.0f} TFLOP/s ({rate / peak:.1%}), {result[name]['cycles_per_mfma']:.1f} cycles an "
+            f"MFMA, clock {np.median(mhz):.0f} MHz ({mhz.min():.0f}-{mhz.max():.0f})")  # fmt: skip
+        ops.close()
+    out.close()
+    stamps.close()
+    return result
+
+
+TRAFFIC = ROOT / "profiles" / "traffic_workloads.md"
 
 
 def measured_traffic(kernel: str) -> dict | None:
-    """HBM bytes per launch of `kernel` on the 4096^3 bf16 problem, as the committed counter passes found them: the
-    summary's `traffic:` line (kernel name, FETCH bytes, WRITE bytes, both already scaled by the copy). None when the
-    summary is absent or measured another kernel."""
+    """HBM-side bytes per launch of `kernel` on the 4096^3 bf16 problem, as the committed counter passes found them
+    (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over `bench.py --only counters`): the summary's `traffic:` line
+    (kernel name, FETCH bytes, WRITE bytes, both already scaled by the copy). None when the summary is absent or
+    measured another kernel."""
     if not TRAFFIC.exists():
         return None
     for line in TRAFFIC.read_text().splitlines():
@@ -355,80 +456,196 @@ def summarize(directory: Path, last: int) -> None:
             print(f"{name} | {grid} | {len(ns)} | {sum(ns) / len(ns) / 1e3:.1f} | {sum(tail) / len(tail) / 1e3:.1f} | "
                   f"{ns[len(ns) // 2] / 1e3:.1f} | {ns[0] / 1e3:.1f}")  # fmt: skip
     for path in sorted(directory.glob("*_counter_collection.csv")):
-        print(f"{path.name}: dispatch | kernel | grid (threads) | counter | value (KiB) | duration us")
+        dispatches: dict[int, dict] = {}
+        names: list[str] = []
         for r in csv.DictReader(path.open()):
-            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-            print(f"{r['Dispatch_Id']} | {r['Kernel_Name']} | {r['Grid_Size']} | {r['Counter_Name']} | "
-                  f"{float(r['Counter_Value']):.1f} | {us:.1f}")  # fmt: skip
+            d = dispatches.setdefault(int(r["Dispatch_Id"]), {
+                "kernel": r["Kernel_Name"].split("(")[0], "grid": r["Grid_Size"],
+                "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3, "values": {}})  # fmt: skip
+            if r["Counter_Name"] not in names:
+                names.append(r["Counter_Name"])
+            d["values"][r["Counter_Name"]] = d["values"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        derived = mfma_shares(path, names)
+        print(f"{path.name}: dispatch | kernel | grid (threads) | duration us | " + " | ".join(names)
+              + (" | MFMA busy % of GUI active | MFMA busy % of SQ busy" if derived else ""))  # fmt: skip
+        for i in sorted(dispatches):
+            d = dispatches[i]
+            values = " | ".join(f"{d['values'].get(n, float('nan')):.6g}" for n in names)
+            print(f"{i} | {d['kernel']} | {d['grid']} | {d['us']:.1f} | {values}"
+                  + ("".join(f" | {x:.1f}" for x in derived(d["values"])) if derived else ""))  # fmt: skip
 
 
-def cpu_baseline(seconds: float = 12.0) -> dict | None:
-    """The reference's host multiply (cr::tensor::multiply<bf16>, single thread, the reference's own header compiled
-    into oracle/_ref) on a bounded bf16 sample, repeated in blocks, median of the blocks. Falls back to the oracle's
-    restatement (kind "port") where oracle/_ref was not built."""
-    ref = ROOT / "oracle" / "_ref" / "libcairnref.so"
-    port = ROOT / "oracle" / "liboracle.so"
-    n = 384
+def mfma_shares(path: Path, names: list[str]):
+    """Where a pass read SQ_VALU_MFMA_BUSY_CYCLES (per SIMD, summed) with GRBM_GUI_ACTIVE (per XCC, summed) and
+    SQ_BUSY_CYCLES (per shader engine, summed): the MFMA-busy share of the SIMDs' cycles, over the GPU's active
+    cycles (rocprofv3's MfmaUtil: busy / (GUI active of one XCC x SIMDs)) and over the cycles any wave was resident.
+    The XCC, shader-engine and SIMD counts come from the pass's own agent_info.csv."""
+    if not {"SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES"} <= set(names):
+        return None
+    import csv
+
+    info = path.with_name(path.name.replace("_counter_collection.csv", "_agent_info.csv"))
+    agents = [r for r in csv.DictReader(info.open()) if int(r.get("Simd_Count") or 0) > 0] if info.exists() else []
+    if not agents:
+        return None
+    xcc, engines, simds = (int(agents[0][k]) for k in ("Num_Xcc", "Array_Count", "Simd_Count"))
+
+    def shares(v: dict) -> tuple[float, float]:
+        busy = v["SQ_VALU_MFMA_BUSY_CYCLES"]
+        gui = v["GRBM_GUI_ACTIVE"] / xcc * simds
+        resident = v["SQ_BUSY_CYCLES"] / engines * simds
+        return (100 * busy / gui if gui else float("nan"), 100 * busy / resident if resident else float("nan"))
+
+    return shares
+
+
+def host_cpu() -> dict:
+    """The host's CPU model (/proc/cpuinfo's first `model name`) and the cores this process may run on."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"model": model, "cores_usable": usable, "cpu_count": os.cpu_count()}
+
+
+def blocks(call, block_s: float = 2e-3, count: int = 9) -> dict:
+    """Time `call` as CAIRN's perf/measure.py times a function (src/cairn/perf/measure.py:22-59): one untimed call,
+    then the calls a block double until a block lasts at least `block_s`; then `count` blocks of that many calls, and
+    the median block's time a call (with the fastest and slowest)."""
+    call()
+    inner = 1
+    while True:
+        t0 = time.perf_counter()
+        for _ in range(inner):
+            call()
+        if time.perf_counter() - t0 >= block_s or inner >= 1 << 30:
+            break
+        inner *= 2
+    per = []
+    for _ in range(count):
+        t0 = time.perf_counter()
+        for _ in range(inner):
+            call()
+        per.append((time.perf_counter() - t0) / inner)
+    per.sort()
+    return {"median_s": per[count // 2], "min_s": per[0], "max_s": per[-1], "inner": inner, "blocks": count}
+
+
+P = C.c_void_p
+SZ = C.c_size_t
+
+
+def host_libraries() -> tuple[C.CDLL | None, C.CDLL | None]:
+    """The reference's multiply compiled from its own header (oracle/_ref) and the oracle's restatement, where built."""
+    ref, port = ROOT / "oracle" / "_ref" / "libcairnref.so", ROOT / "oracle" / "liboracle.so"
+    r = C.CDLL(str(ref)) if ref.exists() else None
+    o = C.CDLL(str(port)) if port.exists() else None
+    if r is not None:
+        for name in ("ref_mma_bf16", "ref_mma_f32"):
+            getattr(r, name).restype = None
+            getattr(r, name).argtypes = [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ]
+    if o is not None:
+        o.oracle_mma.restype = C.c_int
+        o.oracle_mma.argtypes = [C.c_int, SZ, SZ, SZ, P, SZ, P, SZ, P, SZ]
+        o.oracle_mma_rows.restype = None
+        o.oracle_mma_rows.argtypes = [C.c_int, SZ, SZ, SZ, SZ, P, P, P, P]
+        o.oracle_table.restype, o.oracle_table.argtypes = P, [C.c_int]
+        o.oracle_free.restype, o.oracle_free.argtypes = None, [P]
+        o.oracle_gemm_i8.restype = None
+        o.oracle_gemm_i8.argtypes = [C.c_int, C.c_int, SZ, SZ, SZ, P, SZ, P, SZ, P]
+    return r, o
+
+
+def host_multiply(ref, port, fmt: int, n: int, a: np.ndarray, b: np.ndarray, c: np.ndarray):
+    """c += a b (n x n) on one thread: the reference's multiply<A> where built, else the oracle's restatement; and
+    which it was."""
+    ptrs = (c.ctypes.data_as(P), n * n, a.ctypes.data_as(P), n * n, b.ctypes.data_as(P), n * n)
+    if ref is not None:
+        f = ref.ref_mma_bf16 if fmt == L.BF16 else ref.ref_mma_f32
+        return (lambda: f(n, n, n, *ptrs)), "reference"
+    return (lambda: port.oracle_mma(fmt, n, n, n, *ptrs)), "port"
+
+
+def cpu_baseline(n_bf16: int = 768, n_c1: int = 512, n_i8: int = 512, n_rows: int = 1024,
+                 threads: int | None = None) -> dict | None:  # fmt: skip
+    """The reference's CPU multiply on this host, timed as BASELINE.md's CPU plan says: blocks of at least 2 ms,
+    median of 9 (measure.py's method), single thread as the reference runs, on bounded samples:
+    - bf16 n_bf16^3 NN (the headline's type; `value`, in the metric's TFLOP/s, and the time scaled to 4096^3);
+    - C1, f32 n_c1^3 with a, b ~ U[-1, 1) (the reference's CPU-runnable configuration);
+    - int8 -> int32 n_i8^3: the oracle's exact-integer loop (the reference has no int8 multiply);
+    - the build's own row-parallel variant (not the reference): the same loop's rows split over `threads` threads,
+      bf16 n_rows^3, whose bits equal the single-thread loop's.
+    The reference (`kind` "reference") is its own header compiled into oracle/_ref; where that was not built, the
+    oracle's restatement (`kind` "port"). None when neither library is present."""
+    ref, port = host_libraries()
+    if ref is None and port is None:
+        return None
     rng = np.random.default_rng(1)
+    cpu = host_cpu()
+    n = n_bf16
     a = bf16(rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n)))
     b = bf16(rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n)))
     c = np.zeros((n, n), dtype=np.float32)
-    P = C.c_void_p
-    if ref.exists():
-        lib = C.CDLL(str(ref))
-        f = lib.ref_mma_bf16
-        f.argtypes = [C.c_size_t] * 3 + [P, C.c_size_t, P, C.c_size_t, P, C.c_size_t]  # m, n, k, c, cn, a, an, b, bn
-        call = lambda: f(n, n, n, c.ctypes.data_as(P), n * n, a.ctypes.data_as(P), n * n, b.ctypes.data_as(P), n * n)
-        kind = "reference"
-    elif port.exists():
-        lib = C.CDLL(str(port))
-        f = lib.oracle_mma
-        f.argtypes = [C.c_int] + [C.c_size_t] * 3 + [P, C.c_size_t, P, C.c_size_t, P, C.c_size_t]
-        call = lambda: f(2, n, n, n, c.ctypes.data_as(P), n * n, a.ctypes.data_as(P), n * n, b.ctypes.data_as(P), n * n)
-        kind = "port"
-    else:
-        return None
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        call()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    tflops = 2.0 * n**3 / med / 1e12
-    out = {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": kind,
-           "sample": f"bf16 {n}^3 c += a.b, single thread, {len(times)} calls over ~{seconds:.0f} s, median",
-           "ms_per_call": med * 1e3, "extrapolated_4096_cubed_s": med * (4096 / n) ** 3,
-           "host_cpus": os.cpu_count()}  # fmt: skip
-    out["c1"] = cpu_c1(lib, kind)
+    call, kind = host_multiply(ref, port, L.BF16, n, a, b, c)
+    t = blocks(call)
+    out = {"value": 2.0 * n**3 / t["median_s"] / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": kind,
+           "sample": f"bf16 {n}^3 NN c += a.b, single thread; blocks of >= 2 ms ({t['inner']} calls), median of "
+                     f"{t['blocks']} blocks", "ms_per_call": t["median_s"] * 1e3,
+           "extrapolated_4096_cubed_s": t["median_s"] * (4096 / n) ** 3, "cpu": cpu}  # fmt: skip
+    n = n_c1
+    r1 = np.random.default_rng(512)
+    a1 = r1.uniform(-1, 1, (n, n)).astype(np.float32)
+    b1 = r1.uniform(-1, 1, (n, n)).astype(np.float32)
+    c1 = np.zeros((n, n), dtype=np.float32)
+    call, kind1 = host_multiply(ref, port, L.F32, n, a1, b1, c1)
+    t = blocks(call)
+    out["c1"] = {"value": 2.0 * n**3 / t["median_s"] / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": kind1,
+                 "sample": f"C1: f32 {n}^3 c += a.b, a, b ~ U[-1, 1), single thread, median of {t['blocks']} blocks",
+                 "ms_per_call": t["median_s"] * 1e3}  # fmt: skip
+    if port is None:
+        return out
+    n = n_i8
+    ai = rng.integers(-127, 128, (n, n), dtype=np.int8)
+    bi = rng.integers(-127, 128, (n, n), dtype=np.int8)
+    ci = np.zeros((n, n), dtype=np.int32)
+    t = blocks(lambda: port.oracle_gemm_i8(0, 0, n, n, n, ai.ctypes.data_as(P), n, bi.ctypes.data_as(P), n,
+                                           ci.ctypes.data_as(P)))  # fmt: skip
+    out["int8"] = {"value": 2.0 * n**3 / t["median_s"] / 1e9, "unit": "GOP/s", "cores": 1, "kind": "port",
+                   "sample": f"int8 -> int32 {n}^3 NN, exact, single thread, median of {t['blocks']} blocks (the "
+                             "build's own exact-integer loop: the reference has no int8 multiply)",
+                   "ms_per_call": t["median_s"] * 1e3}  # fmt: skip
+    out["row_parallel"] = row_parallel(port, n_rows, threads or min(cpu["cores_usable"] or 1, 16), rng)
     return out
 
 
-def cpu_c1(lib: C.CDLL, kind: str, n: int = 512, calls: int = 5) -> dict:
-    """C1: the f32 512^3 host multiply (the reference's multiply<float>, or the oracle's restatement), single
-    thread, a ~ U[-1, 1), c = 0, median of `calls` calls, in GFLOP/s. The one configuration the reference runs
-    on the CPU alone; it has no GPU roofline."""
-    P = C.c_void_p
-    rng = np.random.default_rng(512)
-    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
-    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+def row_parallel(port, n: int, threads: int, rng) -> dict:
+    """The build's own row-parallel variant of the reference loop (oracle_mma_rows; not the reference): bf16 n^3,
+    rows split evenly over `threads` threads (ctypes releases the GIL for each call), timed as cpu_baseline times."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    a = bf16(rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n)))
+    b = bf16(rng.standard_normal((n, n), dtype=np.float32) / np.float32(np.sqrt(n)))
     c = np.zeros((n, n), dtype=np.float32)
-    if kind == "reference":
-        f = lib.ref_mma_f32
-        f.argtypes = [C.c_size_t] * 3 + [P, C.c_size_t, P, C.c_size_t, P, C.c_size_t]
-        call = lambda: f(n, n, n, c.ctypes.data_as(P), n * n, a.ctypes.data_as(P), n * n, b.ctypes.data_as(P), n * n)
-    else:
-        f = lib.oracle_mma
-        f.argtypes = [C.c_int] + [C.c_size_t] * 3 + [P, C.c_size_t, P, C.c_size_t, P, C.c_size_t]
-        call = lambda: f(0, n, n, n, c.ctypes.data_as(P), n * n, a.ctypes.data_as(P), n * n, b.ctypes.data_as(P), n * n)
-    times = []
-    for _ in range(calls):
-        t0 = time.perf_counter()
-        call()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    return {"value": 2.0 * n**3 / med / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": kind,
-            "sample": f"f32 {n}^3 c += a.b, single thread, median of {calls} calls", "ms_per_call": med * 1e3}
+    table = port.oracle_table(L.BF16)
+    cuts = [n * t // threads for t in range(threads + 1)]
+    pa, pb, pc = a.ctypes.data_as(P), b.ctypes.data_as(P), c.ctypes.data_as(P)
+    with ThreadPoolExecutor(threads) as pool:
+
+        def call():
+            list(pool.map(lambda t: port.oracle_mma_rows(L.BF16, cuts[t], cuts[t + 1], n, n, pc, pa, pb, table),
+                          range(threads)))  # fmt: skip
+
+        t = blocks(call)
+    port.oracle_free(table)
+    return {"value": 2.0 * n**3 / t["median_s"] / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "label": "build's own, not the reference",
+            "sample": f"bf16 {n}^3 NN c += a.b, rows split over {threads} threads, median of {t['blocks']} blocks",
+            "ms_per_call": t["median_s"] * 1e3}  # fmt: skip
 
 
 def main() -> int:
@@ -436,8 +653,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=400)
-    ap.add_argument("--only", choices=["square", "skinny", "mlp", "split", "quantize", "all", "traffic", "calibrate"],
-                    default="all")  # fmt: skip
+    ap.add_argument("--only", default="all", choices=["square", "skinny", "mlp", "split", "quantize", "all", "calibrate",
+                                                      "counters", "ceiling"])  # fmt: skip
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--family", choices=["wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
@@ -459,8 +676,12 @@ def main() -> int:
                           "skinny": bench_skinny(stream, args.steps, args.warmup), "device": dev}), flush=True)  # fmt: skip
         stream.close()
         return 0
-    if args.only == "traffic":
-        print(json.dumps({"traffic_run": bench_traffic(stream, family=args.family)}), flush=True)
+    if args.only == "counters":
+        print(json.dumps({"counters_run": bench_counters(stream)}), flush=True)
+        stream.close()
+        return 0
+    if args.only == "ceiling":
+        print(json.dumps({"ceiling": bench_ceiling(stream, args.steps, args.warmup), "device": dev}), flush=True)
         stream.close()
         return 0
     record = {"metric": "bf16 GEMM TFLOP/s at 4096^3 + int8 TOPS, % of MFMA peak, 1 MI355X", "unit": "TFLOP/s",
@@ -477,6 +698,8 @@ def main() -> int:
                               "frac": bf["kernel_tflops"] / PEAK_BF16,
                               "traffic": traffic["bytes"] if traffic else None,
                               "algorithmic_bytes": 3 * 4096 * 4096 * 2, "kernel": bf["kernel"]}  # fmt: skip
+        # The counters need passes of their own (rocprofv3 --pmc): traffic is that pass's reading, not this run's.
+        record["roofline"]["traffic_measured_in_run"] = False
         if traffic:
             record["roofline"]["traffic_split"] = {"fetch": traffic["fetch"], "write": traffic["write"],
                                                    "source": str(TRAFFIC.relative_to(ROOT))}  # fmt: skip

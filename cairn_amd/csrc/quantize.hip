@@ -12,6 +12,7 @@
 // midpoint of the grid settled from the neighbouring codes (convert_f8), and the integer steps for saturation and
 // special values.
 #include <hip/hip_runtime.h>
+#include <cstdio>
 #include "../../include/cairn_gemm.h"
 #include "quantize.hpp"
 
@@ -479,31 +480,72 @@ hipError_t launch_x(int qt, const cairn::quant::Params& p, bool vec, unsigned ro
   return launch<XT, CAIRN_TYPE_F8E5M2>(p, vec, rows, s);
 }
 
-}  // namespace
-
-extern "C" int cairn_quantize_run(const cairn_quantize_desc* d, void* stream) {
+// The checks cairn_quantize_run makes before it launches: CAIRN_OK with `vec` (whole aligned 8-element chunks, the
+// fast kernel's form) set, or the refusal.
+int checked(const cairn_quantize_desc* d, bool& vec) {
   if(!d || d->version != CAIRN_QUANTIZE_DESC_VERSION) return CAIRN_E_ARG;
   const int xt = d->x_type, qt = d->q_type;
   if(xt != CAIRN_TYPE_F32 && xt != CAIRN_TYPE_F16 && xt != CAIRN_TYPE_BF16) return CAIRN_E_TYPE;
   if(qt != CAIRN_TYPE_I8 && qt != CAIRN_TYPE_F8E4M3 && qt != CAIRN_TYPE_F8E5M2) return CAIRN_E_TYPE;
   if(d->mode != CAIRN_SCALE_ROW_ABSMAX && d->mode != CAIRN_SCALE_ROW && d->mode != CAIRN_SCALE_TENSOR) return CAIRN_E_ARG;
-  if(d->m == 0) return CAIRN_OK;
+  if(d->m == 0) return CAIRN_OK;  // nothing to launch
   const std::uint64_t ldx = d->ldx ? d->ldx : d->k, ldq = d->ldq ? d->ldq : d->k;
   // A row is addressed through a buffer range of k elements: k * 4 bytes must fit its 31-bit offsets.
   if(d->m > 0x7fffffffu || d->k > (1ull << 28) || ldx < d->k || ldq < d->k || ldx > (1ull << 40) || ldq > (1ull << 40))
     return CAIRN_E_SHAPE;
   if(!d->scale || (d->k && (!d->x || !d->q))) return CAIRN_E_ARG;
-  const int xs = xt == CAIRN_TYPE_F32 ? 4 : 2;
-  const bool vec = d->k % 8 == 0 && ldx % 8 == 0 && ldq % 8 == 0 && reinterpret_cast<std::uintptr_t>(d->x) % 16 == 0 &&
-                   reinterpret_cast<std::uintptr_t>(d->q) % 8 == 0;
-  (void)xs;
+  vec = d->k % 8 == 0 && ldx % 8 == 0 && ldq % 8 == 0 && reinterpret_cast<std::uintptr_t>(d->x) % 16 == 0 &&
+        reinterpret_cast<std::uintptr_t>(d->q) % 8 == 0;
+  return CAIRN_OK;
+}
+
+const char* type_name(int t) {
+  switch(t) {
+    case CAIRN_TYPE_F32: return "f32";
+    case CAIRN_TYPE_F16: return "f16";
+    case CAIRN_TYPE_BF16: return "bf16";
+    case CAIRN_TYPE_I8: return "i8";
+    case CAIRN_TYPE_F8E4M3: return "f8e4m3";
+    default: return "f8e5m2";
+  }
+}
+
+}  // namespace
+
+extern "C" int cairn_quantize_run(const cairn_quantize_desc* d, void* stream) {
+  bool vec = false;
+  if(const int s = checked(d, vec); s != CAIRN_OK) return s;
+  if(d->m == 0) return CAIRN_OK;
+  const std::uint64_t ldx = d->ldx ? d->ldx : d->k, ldq = d->ldq ? d->ldq : d->k;
   const cairn::quant::Params p{d->x,          d->q,          d->scale,           d->status,          std::int64_t(d->m),
                                std::int64_t(d->k), std::int64_t(ldx), std::int64_t(ldq), d->mode};
   const auto s = static_cast<hipStream_t>(stream);
   const unsigned rows = unsigned(d->m);
   hipError_t e;
-  if(xt == CAIRN_TYPE_F32) e = launch_x<CAIRN_TYPE_F32>(qt, p, vec, rows, s);
-  else if(xt == CAIRN_TYPE_F16) e = launch_x<CAIRN_TYPE_F16>(qt, p, vec, rows, s);
-  else e = launch_x<CAIRN_TYPE_BF16>(qt, p, vec, rows, s);
+  if(d->x_type == CAIRN_TYPE_F32) e = launch_x<CAIRN_TYPE_F32>(d->q_type, p, vec, rows, s);
+  else if(d->x_type == CAIRN_TYPE_F16) e = launch_x<CAIRN_TYPE_F16>(d->q_type, p, vec, rows, s);
+  else e = launch_x<CAIRN_TYPE_BF16>(d->q_type, p, vec, rows, s);
   return e == hipSuccess ? CAIRN_OK : CAIRN_E_HIP;
+}
+
+extern "C" const char* cairn_quantize_kernel(const cairn_quantize_desc* d) {
+  bool vec = false;
+  if(checked(d, vec) != CAIRN_OK || d->m == 0) return nullptr;
+  // One name a form: the kernel family, the element types, and the rows a workgroup (4 short rows, 1 long one).
+  static char names[2][3][3][2][40];
+  static const bool made = [] {
+    const int xs[3] = {CAIRN_TYPE_F32, CAIRN_TYPE_F16, CAIRN_TYPE_BF16};
+    const int qs[3] = {CAIRN_TYPE_I8, CAIRN_TYPE_F8E4M3, CAIRN_TYPE_F8E5M2};
+    for(int v = 0; v < 2; ++v)
+      for(int x = 0; x < 3; ++x)
+        for(int q = 0; q < 3; ++q)
+          for(int r = 0; r < 2; ++r)
+            std::snprintf(names[v][x][q][r], sizeof names[v][x][q][r], "%s<%s, %s, %d>",
+                          v ? "quantize_fast" : "quantize_rows", type_name(xs[x]), type_name(qs[q]), r ? 1 : 4);
+    return true;
+  }();
+  (void)made;
+  const int x = d->x_type == CAIRN_TYPE_F32 ? 0 : d->x_type == CAIRN_TYPE_F16 ? 1 : 2;
+  const int q = d->q_type == CAIRN_TYPE_I8 ? 0 : d->q_type == CAIRN_TYPE_F8E4M3 ? 1 : 2;
+  return names[vec][x][q][std::int64_t(d->k) > cairn::quant::SHORT];
 }

@@ -138,6 +138,7 @@ SIGNATURES = {
     "cairn_gemm_mma": (C.c_int, [C.c_int32, SZ, SZ, SZ, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "cairn_gemm_device_stream": (None, [C.c_void_p]),
     "cairn_quantize_run": (C.c_int, [C.POINTER(QuantizeDesc), C.c_void_p]),
+    "cairn_quantize_kernel": (C.c_char_p, [C.POINTER(QuantizeDesc)]),
     **{f"cf_mma_{f}": (None, _MMA) for f in ("f32", "f16", "bf16", "f8e4m3", "f8e5m2")},
     **{f"cf_mma_{f}_device": (None, _MMA) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
     **{f"cq_mma_{f}_device": (None, [C.c_void_p, *_MMA]) for f in ("f16", "bf16", "f8e4m3", "f8e5m2")},
@@ -201,6 +202,12 @@ def quantize(d: QuantizeDesc, stream: int | None = None) -> None:
     s = load().cairn_quantize_run(C.byref(d), stream)
     if s != OK:
         raise GemmError(s, status_string(s))
+
+
+def quantize_kernel(d: QuantizeDesc) -> str | None:
+    """The name of the kernel cairn_quantize_run launches for `d` (None: refused, or nothing to launch)."""
+    name = load().cairn_quantize_kernel(C.byref(d))
+    return name.decode() if name else None
 
 
 def select(d: Desc) -> dict:

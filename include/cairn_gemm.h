@@ -114,8 +114,8 @@ typedef struct cairn_gemm_kernel {
   int32_t tile_m, tile_n, tile_k; /* output tile and k-step, in elements */
   int32_t threads;       /* per workgroup */
   int32_t lds_bytes;     /* per workgroup */
-  int32_t family;        /* 0: MFMA tiled, 1: generic (any shape), 2: skinny (m <= 16, bandwidth), 3: pipelined,
-                            4: pipelined, one wave a SIMD */
+  int32_t family;        /* 0: MFMA tiled, 1: generic (any shape), 2: skinny (m <= 16, bandwidth), 4: wave
+                            (256 x 256 pipelined, one wave a SIMD); 3 is not used */
   char name[48];
 } cairn_gemm_kernel;
 
@@ -238,6 +238,10 @@ typedef struct cairn_quantize_desc {
 } cairn_quantize_desc;
 
 int cairn_quantize_run(const cairn_quantize_desc* d, void* stream);
+
+/* The kernel cairn_quantize_run launches for `d`, by name (as a profiler lists it, with its types and rows a
+ * workgroup, e.g. "quantize_fast<bf16, i8, 4>"), or NULL where it refuses `d` or has nothing to launch. No GPU call. */
+const char* cairn_quantize_kernel(const cairn_quantize_desc* d);
 /* cairn:stated-end */
 
 /*
@@ -249,7 +253,7 @@ int cairn_quantize_run(const cairn_quantize_desc* d, void* stream);
  * the build refuses a header whose identity is stale. A translation unit that uses the header's types without the
  * library (a host-only test machine, or an emulated build: CAIRN_EMULATE) defines CAIRN_GEMM_UNLINKED.
  */
-#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_5e01d71c3bad89c7
+#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_b5e647068caf98df
 extern const char CAIRN_GEMM_IDENTITY[];
 #if !defined(CAIRN_GEMM_UNLINKED) && !defined(CAIRN_EMULATE)
 static const char* const cairn_interface_of_gemm_gfx950 __attribute__((used)) = CAIRN_GEMM_IDENTITY;

@@ -304,3 +304,19 @@ def test_the_bindings_use_the_headers_descriptor_versions():
     text = HEADER.read_text()
     assert int(re.search(r"#define CAIRN_GEMM_DESC_VERSION (\d+)u", text).group(1)) == L.DESC_VERSION
     assert int(re.search(r"#define CAIRN_QUANTIZE_DESC_VERSION (\d+)u", text).group(1)) == L.QUANTIZE_DESC_VERSION
+
+
+def test_the_quantize_kernel_query_names_the_launch_form():
+    """cairn_quantize_kernel, no GPU call: the fast kernel for whole aligned 8-element chunks, the general one
+    otherwise; 4 rows a workgroup up to 4096 elements a row, 1 beyond; nothing for m = 0 or a refused descriptor."""
+    X, Q, S = 1 << 20, 1 << 21, 1 << 22  # addresses only: nothing is read
+    assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 8192, 4096, X, Q, S)) == "quantize_fast<bf16, i8, 4>"
+    assert L.quantize_kernel(L.quantize_desc(L.F32, L.F8E4M3, 8, 4096, X, Q, S)) == "quantize_fast<f32, f8e4m3, 4>"
+    assert L.quantize_kernel(L.quantize_desc(L.F32, L.F8E4M3, 8, 4104, X, Q, S)) == "quantize_fast<f32, f8e4m3, 1>"
+    assert L.quantize_kernel(L.quantize_desc(L.F16, L.F8E5M2, 8, 8200, X, Q, S)) == "quantize_fast<f16, f8e5m2, 1>"
+    assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 8, 4096, X + 2, Q, S)) == "quantize_rows<bf16, i8, 4>"
+    assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 8, 4092, X, Q, S)) == "quantize_rows<bf16, i8, 4>"
+    assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 8, 4096, X, Q, S, ldx=4100)) == "quantize_rows<bf16, i8, 4>"
+    assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 0, 4096, X, Q, S)) is None
+    assert L.quantize_kernel(L.quantize_desc(L.BF16, L.F16, 8, 4096, X, Q, S)) is None
+    assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 8, 4096, X, Q, None)) is None
