@@ -44,28 +44,45 @@ __device__ __forceinline__ void col_terms(const Params& p, int n0, int lane, flo
   }
 }
 
-// The epilogue's steps on one accumulator value, each an f32 rounding, in the order cairn_gemm.h states. ACT is a
-// template argument: callers branch on p.act once, outside their loops, so that a loop holds only its own
-// activation's code (256 unrolled copies of GELU that a plain store jumps over still crowd the instruction cache).
-// ACT_SCALES: no activation and no bias (the W8A8 dequant), so the bias step, an add of -0 that changes no value,
-// is left out.
+// The epilogue's form for one launch: its activation (ACT_SCALES: scales and nothing else, the W8A8 dequant, so the
+// bias step, an add of -0 that changes no value, is left out) and whether a row or column scale is present (without
+// one, the two multiplies by 1, which change no value either, are left out). Template arguments: callers branch on
+// the form once, outside their loops, so that a loop holds only its own form's code (256 unrolled copies of GELU that
+// a plain store jumps over still crowd the instruction cache).
 constexpr int ACT_SCALES = -1;
-template<int ACT>
+template<int ACT, bool SCALED> struct Form {
+  static constexpr int act = ACT;
+  static constexpr bool scaled = SCALED;
+};
+
+// The epilogue's steps on one accumulator value, each an f32 rounding, in the order cairn_gemm.h states.
+template<class F>
 __device__ __forceinline__ float apply(float v, float rs, float cs, float bs) {
-  v = v * rs;
-  v = v * cs;
-  if constexpr(ACT != ACT_SCALES) v = v + bs;
-  if constexpr(ACT == CAIRN_ACT_RELU) v = v < 0.0f ? 0.0f : v;
-  else if constexpr(ACT == CAIRN_ACT_GELU) v = gelu(v);
+  if constexpr(F::scaled) {
+    v = v * rs;
+    v = v * cs;
+  }
+  if constexpr(F::act != ACT_SCALES) v = v + bs;
+  if constexpr(F::act == CAIRN_ACT_RELU) v = v < 0.0f ? 0.0f : v;
+  else if constexpr(F::act == CAIRN_ACT_GELU) v = gelu(v);
   return v;
 }
 
-// f(integral_constant<ACT>) for the activation p.act names, ACT_SCALES where there is neither activation nor bias.
-template<class F> __device__ __forceinline__ void with_act(const Params& p, F&& f) {
-  if(p.act == CAIRN_ACT_GELU) f(std::integral_constant<int, CAIRN_ACT_GELU>{});
-  else if(p.act == CAIRN_ACT_RELU) f(std::integral_constant<int, CAIRN_ACT_RELU>{});
-  else if(!p.bias) f(std::integral_constant<int, ACT_SCALES>{});
-  else f(std::integral_constant<int, CAIRN_ACT_NONE>{});
+// f(Form<...>{}) for the activation p.act names (ACT_SCALES where there is neither activation nor bias). GELU without
+// scales (the MLP forward's bias + GELU) has a form of its own; the other forms keep the multiplies, whose cost is
+// small beside their code: each form is another unrolled copy of the epilogue in every kernel, and more copies crowd
+// the registers the main loop needs.
+template<class G> __device__ __forceinline__ void with_form(const Params& p, G&& f) {
+  if(p.act == CAIRN_ACT_GELU) {
+    if(p.row_scale || p.col_scale) f(Form<CAIRN_ACT_GELU, true>{});
+    else f(Form<CAIRN_ACT_GELU, false>{});
+  } else if(p.act == CAIRN_ACT_RELU) {
+    f(Form<CAIRN_ACT_RELU, true>{});
+  } else if(!p.bias) {
+    f(Form<ACT_SCALES, true>{});
+  } else {
+    f(Form<CAIRN_ACT_NONE, true>{});
+  }
 }
 
 // RAW: the int32 accumulator itself is the output (int8 operands, c of int32, no epilogue); the kernel is built once
@@ -93,8 +110,8 @@ __device__ __forceinline__ void finish(const Params& p, const Acc (&acc)[FM][FN]
       return;
     }
   } else {
-  with_act(p, [&](auto act) {
-  constexpr int ACT = decltype(act)::value;
+  with_form(p, [&](auto form) {
+  using F = decltype(form);
   float rs[FM];
   row_scales<FM>(p, r0, lane, rs);
 #pragma unroll
@@ -109,7 +126,7 @@ __device__ __forceinline__ void finish(const Params& p, const Acc (&acc)[FM][FN]
         if(!whole && !(m < p.m && n < p.n)) continue;
         float v[4];
 #pragma unroll
-        for(int e = 0; e < 4; ++e) v[e] = apply<ACT>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
+        for(int e = 0; e < 4; ++e) v[e] = apply<F>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
         const std::int64_t at = std::int64_t(m) * p.ldc + n;
         if(p.c_type == CAIRN_TYPE_F32) {
           float* out = reinterpret_cast<float*>(c + at * 4);

@@ -63,31 +63,32 @@ __device__ inline std::uint16_t narrow_f16(float x) {
 }
 __device__ inline float widen_bf16(std::uint16_t b) { return from_bits(std::uint32_t(b) << 16); }
 
-// GELU in its erf form, 0.5 x (1 + erf(x / sqrt 2)), in f32 and without branches (the library erff takes two paths
-// by |x|, and a wave whose lanes straddle them runs both). 1 + erf(x / sqrt 2) is erfc(z) for x < 0 and 2 - erfc(z)
-// otherwise, z = |x| / sqrt 2, so nothing subtracts near-equal values. erfc(z) is the Chebyshev fit of Press,
-// Teukolsky, Vetterling and Flannery, Numerical Recipes, 2nd ed., section 6.2 (erfcc): t = 1 / (1 + z / 2),
-// erfc(z) = t exp(-z^2 - 1.26551223 + t P(t)), fractional error below 1.2e-7 for every z >= 0. Evaluated in f32 with
-// fused steps, the hardware's reciprocal and 2^x (1 ulp each), and the exponent's -x^2 / 2 formed exactly inside one
-// fma: relative error at most 4.1e-7 for |x| <= 1, 1.8e-6 for |x| <= 6, 7.5e-6 out to |x| = 13, where GELU reaches
-// f32's smallest normals (tests/test_gelu_form.py). The erff form is worse for negative x: its 1 + erf cancels,
-// wholly below x = -5. +inf gives +inf; NaN, and -inf (0 * inf), give NaN, as the erff form does.
+// GELU in its erf form, x Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), in f32 and without branches (the library erff takes
+// two paths by |x|, and a wave whose lanes straddle them runs both). Phi(x) is 1 - h for x >= 0 and h otherwise, with
+// h = Phi(-|x|) = erfc(z) / 2, z = |x| / sqrt 2, so nothing subtracts near-equal values. h is written
+// t 2^(q(t) - z^2 log2 e) with t = 1 / (1 + P z): q(t) = log2(erfcx(z) (1 + P z)) - 1 is smooth on t in (0, 1], and
+// its degree-8 polynomial below is this build's minimax fit (iteratively reweighted least squares against scipy's
+// erfcx, P = 0.38, over |x| <= 13.2, each coefficient rounded to f32 before the lower ones were refitted): absolute
+// error 9.4e-8, so h keeps a relative error of that size for every x
+// (the form of Press, Teukolsky, Vetterling and Flannery, Numerical Recipes, 2nd ed., section 6.2, erfcc, with a
+// shorter fit). Evaluated in f32 with fused steps, the hardware's reciprocal and 2^x (1 ulp each), and the
+// exponent's -z^2 log2 e inside one fma: relative error at most 4.6e-7 for |x| <= 1, 1.9e-6 for |x| <= 6, 7.7e-6 out
+// to |x| = 13, where GELU reaches f32's smallest normals (tests/test_gelu_form.py). 20 instructions a value, two of
+// them the reciprocal and 2^x. +inf gives +inf; NaN, and -inf (0 * inf), give NaN, as the erff form does.
 __device__ inline float gelu(float x) {
-  const float z = __builtin_fabsf(x) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
-  float p = 0.17087277f;
-  p = __builtin_fmaf(p, t, -0.82215223f);
-  p = __builtin_fmaf(p, t, 1.48851587f);
-  p = __builtin_fmaf(p, t, -1.13520398f);
-  p = __builtin_fmaf(p, t, 0.27886807f);
-  p = __builtin_fmaf(p, t, -0.18628806f);
-  p = __builtin_fmaf(p, t, 0.09678418f);
-  p = __builtin_fmaf(p, t, 0.37409196f);
-  p = __builtin_fmaf(p, t, 1.00002368f);
-  p = __builtin_fmaf(p, t, -1.26551223f);
-  const float arg = __builtin_fmaf(-x, 0.5f * x, p);  // -z^2 + t P(t) - 1.26551223, the square exact
-  const float e = t * __builtin_amdgcn_exp2f(arg * 1.44269504088896340736f);
-  return 0.5f * x * (x >= 0.0f ? 2.0f - e : e);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_fabsf(x), 0.268700577f, 1.0f));  // P / sqrt 2
+  float q = -0.35370594f;
+  q = __builtin_fmaf(q, t, 1.7261575f);
+  q = __builtin_fmaf(q, t, -3.1757226f);
+  q = __builtin_fmaf(q, t, 2.7078722f);
+  q = __builtin_fmaf(q, t, -1.4281899f);
+  q = __builtin_fmaf(q, t, 0.77864224f);
+  q = __builtin_fmaf(q, t, 0.5123964f);
+  q = __builtin_fmaf(q, t, 1.4548278f);
+  q = __builtin_fmaf(q, t, -3.2222776f);
+  const float arg = __builtin_fmaf(-x, x * 0.721347520f, q);  // q - x^2 (log2 e) / 2
+  const float h = t * __builtin_amdgcn_exp2f(arg);
+  return x * (x >= 0.0f ? 1.0f - h : h);
 }
 
 // The epilogue of the outputs (m, n0 .. n0+count-1) of one row, on f32 values v: each step an f32 rounding, in this

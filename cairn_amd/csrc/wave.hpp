@@ -137,8 +137,8 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
               put(i, j, q, float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]), float(acc[i][j][4 * q + 2]),
                   float(acc[i][j][4 * q + 3]));
       } else {
-        with_act(p, [&](auto act) {
-          constexpr int ACT = decltype(act)::value;
+        with_form(p, [&](auto form) {
+          using F = decltype(form);
           float rs[FM];
 #pragma unroll
           for(int i = 0; i < FM; ++i) rs[i] = terms[wr + 32 * i + (lane & 31)];
@@ -159,7 +159,7 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
               for(int q = 0; q < 4; ++q) {
                 float v[4];
 #pragma unroll
-                for(int e = 0; e < 4; ++e) v[e] = apply<ACT>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
+                for(int e = 0; e < 4; ++e) v[e] = apply<F>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
                 put(i, j, q, v[0], v[1], v[2], v[3]);
               }
           }
@@ -730,8 +730,8 @@ __global__ void __launch_bounds__(256) split_fixup(Params p) {
     *reinterpret_cast<u32x4*>(c + at * 4) = sum;
     return;
   }
-  with_act(p, [&](auto act) {
-    constexpr int ACT = decltype(act)::value;
+  with_form(p, [&](auto form) {
+    using F = decltype(form);
     const float rs = p.row_scale ? p.row_scale[m] : 1.0f;
     float v[4];
 #pragma unroll
@@ -741,7 +741,7 @@ __global__ void __launch_bounds__(256) split_fixup(Params p) {
       const float bs = !p.bias ? -0.0f
                        : p.bias_type == CAIRN_TYPE_BF16 ? widen_bf16(static_cast<const std::uint16_t*>(p.bias)[n + e])
                                                         : static_cast<const float*>(p.bias)[n + e];
-      v[e] = apply<ACT>(acc, rs, cs, bs);
+      v[e] = apply<F>(acc, rs, cs, bs);
     }
     if(p.c_type == CAIRN_TYPE_F32) {
       float* out = reinterpret_cast<float*>(c + at * 4);
