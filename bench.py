@@ -364,6 +364,38 @@ def bench_counters(stream, launches: int = 3) -> dict:
     return {"order": order, "copy_bytes": COPY_BYTES}
 
 
+def bench_selector(stream, reps: int = 20, warmup: int = 20) -> dict:
+    """The selector's ranking of the tiled families, measured: the 256 x 256 one-wave-a-SIMD kernel and the 128 x 128
+    MFMA kernel, each named, on a sweep of NN shapes (m, n from 256 to 4096, k = 1024 and 4096; bf16 into bf16 and
+    int8 into int32), random operands, each a burst of `reps` launches after `warmup`; with the kernel the selector
+    picks."""
+    rng = np.random.default_rng(5)
+    big = 4096
+    sizes = [256, 768, 1536, 2048, 3072, 4096]
+    out = []
+    for ab, out_type, tag in ((L.BF16, L.BF16, "bf16"), (L.I8, L.I32, "i8")):
+        a = hip.Buffer.of(operands(ab, (big, big), rng))
+        b = hip.Buffer.of(operands(ab, (big, big), rng))
+        c = hip.Buffer(big * big * 4)
+        wave, mfma = L.kernel_named(f"cairn_wave_{tag}_nn_256x256"), L.kernel_named(f"cairn_mfma_{tag}_nn_128x128")
+        for k in (1024, 4096):
+            for m in sizes:
+                for n in sizes:
+                    d = L.desc(ab, out_type, m, n, k, a.ptr, b.ptr, c.ptr, lda=big, ldb=big, ldc=big)
+                    pick = L.select(d)["name"]
+                    d.kernel = wave
+                    tw = timed([d], stream, reps, warmup, reps=1)["event_ms_per_step"] * 1e3
+                    d.kernel = mfma
+                    tm = timed([d], stream, reps, warmup, reps=1)["event_ms_per_step"] * 1e3
+                    out.append({"type": tag, "m": m, "n": n, "k": k, "wave_us": round(tw, 2), "mfma_us": round(tm, 2),
+                                "pick": pick})  # fmt: skip
+        log(f"selector sweep {tag}: wave faster on {sum(r['wave_us'] <= r['mfma_us'] for r in out if r['type'] == tag)}"
+            f" of {sum(r['type'] == tag for r in out)} shapes")  # fmt: skip
+        for x in (a, b, c):
+            x.close()
+    return {"shapes": out}
+
+
 CEILING = ROOT / "tests" / "cpp" / "libmfma_ceiling.so"
 
 
@@ -654,7 +686,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--only", default="all", choices=["square", "skinny", "mlp", "split", "quantize", "all", "calibrate",
-                                                      "counters", "ceiling"])  # fmt: skip
+                                                      "counters", "ceiling", "selector"])  # fmt: skip
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--family", choices=["wave"], help="run the square GEMMs on this kernel family")
     ap.add_argument("--summarize", type=Path, help="print tables from a rocprofv3 CSV output folder and exit")
@@ -678,6 +710,10 @@ def main() -> int:
         return 0
     if args.only == "counters":
         print(json.dumps({"counters_run": bench_counters(stream)}), flush=True)
+        stream.close()
+        return 0
+    if args.only == "selector":
+        print(json.dumps({"selector": bench_selector(stream), "device": dev}), flush=True)
         stream.close()
         return 0
     if args.only == "ceiling":

@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <cstddef>
 #include <cstring>
+#include <initializer_list>
 #include "../../include/cairn_gemm.h"
 #include "kernels.hpp"
 
@@ -180,16 +181,6 @@ int resident(const Kernel& k) {
   return std::max(1, std::min(2, LDS_PER_CU / lds));
 }
 
-// The share of the MFMA rate a tile shape sustains, relative to 256 x 256: smaller tiles read more operand bytes per
-// MFMA from LDS and L2. These are the selector's model, refit from the measured rates the benchmark records.
-double shape_rate(const Kernel& k) {
-  const int area = k.bm * k.bn;
-  if(k.family == WAVE) return area >= 256 * 256 ? 2.2 : (area >= 256 * 128 ? 1.9 : 1.6);
-  if(area >= 256 * 256) return 1.0;
-  if(area >= 256 * 128) return 0.92;
-  return 0.78;
-}
-
 // k elements a k-step of the kernel covers.
 int tile_k(const Kernel& k) {
   const int bytes = k.family == MFMA ? 128 : (ring(k) ? 64 : 32);
@@ -252,7 +243,7 @@ Plan plan_of(const cairn_gemm_desc& d, const Kernel& k, std::uint64_t room) {
 std::uint64_t room_of(const cairn_gemm_desc& d) { return d.workspace ? d.workspace_bytes : 0; }
 
 struct Estimate {
-  double cost, waves, efficiency;
+  double waves, efficiency;
   std::uint64_t workgroups;
 };
 
@@ -264,7 +255,6 @@ Estimate estimate(const cairn_gemm_desc& d, const Kernel& k, const Plan& plan) {
     e.workgroups = blocks;
     e.waves = double(blocks) / CUS;  // one workgroup of four waves a CU
     e.efficiency = 1.0;
-    e.cost = 1.0;
     return e;
   }
   const std::uint64_t tm = (d.m + k.bm - 1) / k.bm, tn = (d.n + k.bn - 1) / k.bn;
@@ -274,15 +264,21 @@ Estimate estimate(const cairn_gemm_desc& d, const Kernel& k, const Plan& plan) {
                                          : std::ceil(double(tiles) / double(slots));
   e.workgroups = plan.split.tiles ? plan.whole + std::uint64_t(plan.split.xcds) * plan.split.units : tiles;
   e.waves = double(tiles) / double(slots);
-  // Time: rounds of resident tiles, each round a tile's k-loop at the shape's rate (resident tiles share a CU).
-  e.cost = rounds * double(k.bm) * double(k.bn) * resident(k) / shape_rate(k);
   const double useful = double(d.m) * double(d.n);
   e.efficiency = useful / (rounds * double(slots) * double(k.bm) * double(k.bn));
   return e;
 }
 
-// The kernel for a checked problem: the named one if it can run it, else the cheapest tiled kernel that fits, else
-// the skinny kernel for a decode-shaped bf16 problem, else the generic kernel.
+// The kernel for a checked problem: the named one if it can run it; else the ring kernel (256 x 256, one wave a SIMD)
+// where its loads fit; else the 128 x 128 MFMA kernel where its chunks fit; else the skinny kernel for a decode-shaped
+// bf16 problem (ahead of both, from m <= 16); else the generic kernel. There is one kernel of each family for a type
+// and layout, so this is a ranking of families, and it is measured, not modelled (`bench.py --only selector`: NN, m
+// and n from 256 to 4096, k = 1024 and 4096, bf16 and int8). The ring kernel was faster at every bf16 shape,
+// including those where its fewer, larger tiles leave most CUs idle: a round of tiles takes about one tile's time
+// however few tiles it holds (idle CUs let the power-limited clock rise), and a lone 256 x 256 tile finishes sooner
+// than a lone 128 x 128 one. int8 is the exception: at k = 1024, wherever the MFMA kernel's tiles fit one to a CU
+// (24 of the 36 int8 shapes at that k), it was faster, 15.7-18.8 us against 17.8-20.3 (int8's stages are half as
+// many, so the larger tile's longer prologue and epilogue weigh more); past one tile a CU, and at k = 4096, it was not.
 int choose(const cairn_gemm_desc& d, int named) {
   if(named) {
     if(named < 1 || named > COUNT) return -CAIRN_E_KERNEL;
@@ -295,15 +291,11 @@ int choose(const cairn_gemm_desc& d, int named) {
     for(int id = 1; id <= COUNT; ++id)
       if(TABLE[id - 1].family == SKINNY) return id;
   }
-  int best = 0;
-  double cost = 0;
-  for(int id = 1; id <= COUNT; ++id) {
-    const Kernel& k = TABLE[id - 1];
-    if(!tiled_fits(d, k)) continue;
-    const double c = estimate(d, k, plan_of(d, k, room_of(d))).cost;
-    if(!best || c < cost) best = id, cost = c;
-  }
-  if(best) return best;
+  const std::uint64_t small_tiles = ((d.m + 127) / 128) * ((d.n + 127) / 128);
+  const bool short_i8 = d.ab_type == CAIRN_TYPE_I8 && d.k <= 1024 && small_tiles <= std::uint64_t(CUS);
+  for(const int family : short_i8 ? std::initializer_list<int>{MFMA, WAVE} : std::initializer_list<int>{WAVE, MFMA})
+    for(int id = 1; id <= COUNT; ++id)
+      if(TABLE[id - 1].family == family && tiled_fits(d, TABLE[id - 1])) return id;
   for(int id = 1; id <= COUNT; ++id)
     if(TABLE[id - 1].family == GENERIC) return id;
   return -CAIRN_E_KERNEL;

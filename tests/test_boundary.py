@@ -320,3 +320,25 @@ def test_the_quantize_kernel_query_names_the_launch_form():
     assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 0, 4096, X, Q, S)) is None
     assert L.quantize_kernel(L.quantize_desc(L.BF16, L.F16, 8, 4096, X, Q, S)) is None
     assert L.quantize_kernel(L.quantize_desc(L.BF16, L.I8, 8, 4096, X, Q, None)) is None
+
+
+def test_the_selector_ranks_the_ring_kernel_first_then_the_mfma_kernel():
+    """One kernel a family for a type and layout: the 256 x 256 ring kernel wherever its loads fit (measured faster at
+    every bf16 shape of `bench.py --only selector`), the 128 x 128 MFMA kernel where only its chunks fit, else generic;
+    and int8 at k <= 1024 with at most 256 MFMA tiles, where the MFMA kernel measured faster, on it."""
+    for ab, tag in ((L.BF16, "bf16"), (L.F16, "f16"), (L.I8, "i8")):
+        out = L.I32 if ab == L.I8 else L.BF16
+        for m, n, k in ((4096, 4096, 4096), (256, 256, 4096), (300, 512, 2048), (8192, 11008, 4096), (4096, 4096, 1024)):
+            assert L.select(L.desc(ab, out, m, n, k, P, P, P))["name"] == f"cairn_wave_{tag}_nn_256x256", (tag, m, n, k)
+        # n = 128: b's k rows (NN, N-major) are closer than a 256-wide tile, too close for the ring's immediate offsets
+        assert L.select(L.desc(ab, out, 4096, 128, 4096, P, P, P))["name"] == f"cairn_mfma_{tag}_nn_128x128"
+        # n = 4: no 16-byte chunk of b's rows; only the generic kernel
+        assert L.select(L.desc(ab, out, 4096, 4, 4096, P, P, P))["name"] == "cairn_generic_64x64"
+    # int8 n = 520: the ring's N-major rows go in 16-byte chunks (16 columns), the MFMA kernel's in 8-byte ones
+    assert L.select(L.desc(L.I8, L.I32, 300, 520, 2048, P, P, P))["name"] == "cairn_mfma_i8_nn_128x128"
+    # int8, k <= 1024, at most 256 tiles of 128 x 128: the MFMA kernel; one tile more, or a longer k: the ring kernel
+    for m, n, k, name in ((2048, 2048, 1024, "mfma"), (256, 4096, 1024, "mfma"), (300, 512, 64, "mfma"),
+                          (2048, 2176, 1024, "wave"), (2048, 2048, 1040, "wave")):
+        assert L.select(L.desc(L.I8, L.I32, m, n, k, P, P, P))["name"] == f"cairn_{name}_i8_nn_" + (
+            "128x128" if name == "mfma" else "256x256"), (m, n, k)
+    assert L.select(L.desc(L.BF16, L.BF16, 2048, 2048, 1024, P, P, P))["name"] == "cairn_wave_bf16_nn_256x256"
