@@ -118,3 +118,18 @@ def test_the_counter_table_has_a_row_a_dispatch_and_a_column_a_counter(tmp_path,
     assert out[0].endswith("duration us | SQ_BUSY_CYCLES | GRBM_GUI_ACTIVE")
     assert out[1] == "1 | wave_gemm<x> | 65536 | 100.0 | 15 | 4"  # a counter's instances summed
     assert out[2] == "2 | copy | 1024 | 100.0 | 3 | nan"
+
+
+def test_the_cpu_leg_child_reports_its_record_or_its_end():
+    """cpu_result's protocol with stand-in children: one that waits for its go and prints a record, one that aborts
+    without a word (as a failed check of the reference's host code does): the bench keeps the record, or the status."""
+    import subprocess
+
+    def child(code: str) -> subprocess.Popen:
+        return subprocess.Popen([sys.executable, "-c", code], stdin=subprocess.PIPE, stdout=subprocess.PIPE,
+                                stderr=subprocess.PIPE, text=True)  # fmt: skip
+
+    ok = bench.cpu_result(child("import sys, json; sys.stdin.readline(); print(json.dumps({'value': 1.5}))"))
+    assert ok == {"value": 1.5}
+    bad = bench.cpu_result(child("import sys, os; sys.stdin.readline(); os.abort()"))
+    assert bad["error"].endswith("status -6")
