@@ -441,8 +441,12 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
                        rows);
     return hipGetLastError();
   }
-  if(p.m > 4 && p.n >= 8192) {  // 64 columns a workgroup (16 a wave); 56 a workgroup over all 256 CUs was slower
-    const int width = 64;
+  if(p.m > 4 && p.n >= 8192) {
+    // Columns a workgroup (16 a wave): n spread evenly over the 256 CUs where that is 56 or more (the decode shape,
+    // n = 14336: 56, all 256 CUs; side by side in one process at m = 16, 4.82 TB/s against 4.68 for 64 columns on
+    // 224 CUs), else 64 (narrower workgroups measured far slower there: 32 columns at n = 8192, 3.3 TB/s).
+    const int even = cairn_skinny_width(p.n);
+    const int width = even >= 56 ? even : 64;
     hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 512>), dim3(unsigned((p.n + width - 1) / width)), dim3(256), 0, s,
                        p, width);
     return hipGetLastError();
