@@ -292,7 +292,7 @@ int choose(const cairn_gemm_desc& d, int named) {
       if(TABLE[id - 1].family == SKINNY) return id;
   }
   const std::uint64_t small_tiles = ((d.m + 127) / 128) * ((d.n + 127) / 128);
-  const bool short_i8 = d.ab_type == CAIRN_TYPE_I8 && d.k <= 1024 && small_tiles <= std::uint64_t(CUS);
+  const bool short_i8 = d.ab_type == CAIRN_TYPE_I8 && d.k > 0 && d.k <= 1024 && small_tiles <= std::uint64_t(CUS);
   for(const int family : short_i8 ? std::initializer_list<int>{MFMA, WAVE} : std::initializer_list<int>{WAVE, MFMA})
     for(int id = 1; id <= COUNT; ++id)
       if(TABLE[id - 1].family == family && tiled_fits(d, TABLE[id - 1])) return id;
