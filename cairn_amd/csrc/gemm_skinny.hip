@@ -420,9 +420,9 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // Four forms, chosen by what measured fastest on the decode shape (n = 14336, k = 4096) in one run of each set:
   // m = 1, whole rows a wave (5.2 TB/s, against 5.1 for the register form and 4.6 for the ring); m = 2 .. 4, the
   // streaming form (side by side in one process: m = 4 4.76 against 4.58 TB/s for the register form, m = 3 4.85
-  // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 8192, the LDS ring
-  // (4.6 against 4.4 TB/s at m = 16, and 4.0 for the streaming form, whose loads of a's 16 rows double the L2
-  // traffic); otherwise the register form.
+  // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 4096, the LDS ring
+  // (4.6 against 4.4 TB/s for the register form at m = 16, and 4.0 for the streaming form, whose loads of a's 16
+  // rows double the L2 traffic); otherwise the register form.
   // Whole rows a wave: 8 waves a CU, 12 from n = 12288 (side by side at n = 14336, k = 4096: 5.41 TB/s against 5.30
   // for 8 a CU, 5.35 for 4 and 5.39 for 16; below n = 12288 8 a CU was fastest at every shape tried).
   const int row_waves = p.n >= 12288 ? 3072 : 2048;
@@ -441,13 +441,17 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
                        rows);
     return hipGetLastError();
   }
-  if(p.m > 4 && p.n >= 8192) {
-    // Columns a workgroup (16 a wave): n spread evenly over the 256 CUs where that is 56 or more (the decode shape,
-    // n = 14336: 56, all 256 CUs; side by side in one process at m = 16, 4.82 TB/s against 4.68 for 64 columns on
-    // 224 CUs), else 64 (narrower workgroups measured far slower there: 32 columns at n = 8192, 3.3 TB/s).
+  if(p.m > 4 && p.n >= 4096) {
+    // The ring with 256-byte stages (80 KiB of LDS, so two workgroups share a CU where there are more than 256).
+    // Columns a workgroup: 32 below n = 8192 (128 .. 224 workgroups); above, n spread evenly over the 256 CUs where
+    // that is 56 or more (the decode shape, n = 14336: 56, all 256 CUs), else 64. Measured side by side on two boxes
+    // at m = 5 .. 16 against the 512-byte ring (64 columns, 160 KiB) and the register form below n = 8192: 9-19%
+    // faster at n = 5120 .. 7168, even at 14336 (4.8 TB/s either way at 56 columns), 2-4% faster at 8192 and 2-15%
+    // from 16384 on, where two workgroups a CU keep every CU streaming. 32 columns where they give 257 .. 511
+    // workgroups (n = 10240 .. 14336) measured far slower.
     const int even = cairn_skinny_width(p.n);
-    const int width = even >= 56 ? even : 64;
-    hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 512>), dim3(unsigned((p.n + width - 1) / width)), dim3(256), 0, s,
+    const int width = p.n < 8192 ? 32 : (even >= 56 ? even : 64);
+    hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 256>), dim3(unsigned((p.n + width - 1) / width)), dim3(256), 0, s,
                        p, width);
     return hipGetLastError();
   }

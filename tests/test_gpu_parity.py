@@ -332,7 +332,7 @@ def test_bias_and_activation_match_the_closed_form(act):
 # ------------------------------------------------------------------ skinny decode shapes
 
 
-@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
 def test_skinny_decode_shapes_keep_the_contract(m):
     rng = np.random.default_rng(100 + m)
     n, k = 14336, 4096
@@ -346,14 +346,16 @@ def test_skinny_decode_shapes_keep_the_contract(m):
     assert H.outside(v, exact, room) == 0
 
 
-# m > 4 with n >= 8192 takes the ring form (64 columns a workgroup, 512-byte stages of k), m = 1 with n >= 2048 and
-# k <= 4096 the row-streaming one (whole rows of b a wave), m = 2 .. 4 with n >= 2048 the streaming MFMA form (16
-# rows of b a wave; whole groups of 8 steps, then single steps, the last one partial), the rest the register form:
-# tails in each.
+# m > 4 with n >= 4096 takes the ring form (256-byte stages of k; 32 columns a workgroup below n = 8192, 56 or 64
+# above, two workgroups a CU past 256 of them), m = 1 with n >= 2048 and k <= 4096 the row-streaming one (whole rows
+# of b a wave), m = 2 .. 4 with n >= 2048 the streaming MFMA form (16 rows of b a wave; whole groups of 8 steps, then
+# single steps, the last one partial), the rest the register form: tails in each.
 @pytest.mark.parametrize("m,n,k", [(1, 8, 8), (3, 100, 72), (16, 33, 4104), (7, 14336, 24), (5, 200, 4160),
                                    (2, 72, 1000), (3, 8200, 4104), (16, 9000, 520), (1, 8192, 8), (9, 8257, 1032),
                                    (1, 4100, 4096), (1, 3000, 1000), (1, 20000, 264), (1, 2048, 4088), (5, 8256, 4096),
-                                   (2, 2048, 8), (4, 3001, 1000), (2, 70001, 40), (4, 2050, 520), (3, 14336, 4096)])
+                                   (2, 2048, 8), (4, 3001, 1000), (2, 70001, 40), (4, 2050, 520), (3, 14336, 4096),
+                                   (8, 4096, 1000), (11, 6150, 264), (6, 20003, 520), (16, 28672, 136),
+                                   (5, 4095, 256)])
 def test_skinny_tails_keep_the_contract(m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = H.normal_bf16(rng, (m, k), 1.0)
