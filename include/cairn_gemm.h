@@ -99,8 +99,10 @@ typedef struct cairn_gemm_desc {
    * share into partial tiles in `workspace`; a fixup pass adds each tile's partials in k order (so the result's bits
    * do not depend on timing) and applies the epilogue. cairn_gemm_workspace says how many bytes the split needs.
    * workspace NULL, or split_units -1: no split. split_units 0: the selector's choice (where it pays, and within
-   * workspace_bytes). The workspace is the caller's device memory, 256-byte aligned, not shared with a call that
-   * may run at the same time. */
+   * workspace_bytes). split_units n > 0: about n units, n / 8 on each XCD (at least one) where the tiles divide
+   * into 8 equal blocks, else n; CAIRN_E_SCRATCH where they need more than workspace_bytes, CAIRN_E_ARG where a unit
+   * would reach into a third tile. The workspace is the caller's device memory, 256-byte aligned, not shared with
+   * a call that may run at the same time. */
   void* workspace;
   uint64_t workspace_bytes;
   int32_t split_units;
@@ -253,7 +255,7 @@ const char* cairn_quantize_kernel(const cairn_quantize_desc* d);
  * the build refuses a header whose identity is stale. A translation unit that uses the header's types without the
  * library (a host-only test machine, or an emulated build: CAIRN_EMULATE) defines CAIRN_GEMM_UNLINKED.
  */
-#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_b5e647068caf98df
+#define CAIRN_GEMM_IDENTITY cairn_interface_gemm_gfx950_15b0d41353760eb5
 extern const char CAIRN_GEMM_IDENTITY[];
 #if !defined(CAIRN_GEMM_UNLINKED) && !defined(CAIRN_EMULATE)
 static const char* const cairn_interface_of_gemm_gfx950 __attribute__((used)) = CAIRN_GEMM_IDENTITY;
