@@ -62,8 +62,8 @@ int op_of(int type) {
     case CAIRN_TYPE_BF16: return cairn::gemm::OP_BF16;
     case CAIRN_TYPE_F16: return cairn::gemm::OP_F16;
     case CAIRN_TYPE_I8: return cairn::gemm::OP_I8;
-    case CAIRN_TYPE_F8E4M3: return cairn::gemm::OP_F8E4M3;  // the fp8 matrix core; the generic kernel widens them
-    case CAIRN_TYPE_F8E5M2: return cairn::gemm::OP_F8E5M2;  // where no tiled kernel fits
+    case CAIRN_TYPE_F8E4M3: return cairn::gemm::OP_F8E4M3;  // the MFMA and generic kernels widen them to f16; the
+    case CAIRN_TYPE_F8E5M2: return cairn::gemm::OP_F8E5M2;  // ring's wave8 form runs the 8-bit float matrix core
     default: return -1;
   }
 }
@@ -118,16 +118,20 @@ int check(const cairn_gemm_desc* in, Problem& out) {
   return CAIRN_OK;
 }
 
-// Can the tiled MFMA kernel take this problem: its 16-byte chunks whole and aligned, its offsets inside int32.
+// Is d's operand type an 8-bit float (which the MFMA kernel widens to f16 on its way into LDS).
+bool float8(int type) { return type == CAIRN_TYPE_F8E4M3 || type == CAIRN_TYPE_F8E5M2; }
+
+// Can the tiled MFMA kernel take this problem: its 16-byte LDS chunks whole and aligned in memory (8 bytes of the
+// 8-bit floats, which widen to 16), its offsets inside int32.
 bool mfma_fits(const cairn_gemm_desc& d, const Kernel& k) {
   if(k.family != MFMA || k.op != op_of(d.ab_type) || k.ta != bool(d.trans_a) || k.tb != bool(d.trans_b)) return false;
-  const int es = element_size(d.ab_type), ce = 16 / es;
+  const int gs = element_size(d.ab_type), es = float8(d.ab_type) ? 2 : gs, ce = 16 / es;
   const std::uint64_t bk = 128 / es;
   auto kmajor = [&](const void* p, std::uint64_t ld, int rows) {
-    return d.k % ce == 0 && ld % ce == 0 && aligned(p, 16) && std::uint64_t(rows) * ld * es < 0x7fff0000ULL;
+    return d.k % ce == 0 && ld % ce == 0 && aligned(p, ce * gs) && std::uint64_t(rows) * ld * gs < 0x7fff0000ULL;
   };
   auto mnmajor = [&](const void* p, std::uint64_t ld, std::uint64_t cols) {
-    return cols % 8 == 0 && ld % 8 == 0 && aligned(p, 8 * es) && bk * ld * es < 0x7fff0000ULL;
+    return cols % 8 == 0 && ld % 8 == 0 && aligned(p, 8 * gs) && bk * ld * gs < 0x7fff0000ULL;
   };
   const bool a_ok = d.trans_a ? mnmajor(d.a, d.lda, d.m) : kmajor(d.a, d.lda, k.bm);
   const bool b_ok = d.trans_b ? kmajor(d.b, d.ldb, k.bn) : mnmajor(d.b, d.ldb, d.n);
@@ -185,7 +189,8 @@ int resident(const Kernel& k) {
 int tile_k(const Kernel& k) {
   const int bytes = k.family == MFMA ? 128 : (ring(k) ? 64 : 32);
   if(k.family == SKINNY) return 32;
-  const bool byte = k.op == cairn::gemm::OP_I8 || k.op == cairn::gemm::OP_F8E4M3 || k.op == cairn::gemm::OP_F8E5M2;
+  const bool f8 = k.op == cairn::gemm::OP_F8E4M3 || k.op == cairn::gemm::OP_F8E5M2;
+  const bool byte = k.op == cairn::gemm::OP_I8 || (f8 && k.family != MFMA);  // the MFMA kernel holds them as f16
   return byte ? bytes : bytes / 2;
 }
 
@@ -293,7 +298,12 @@ int choose(const cairn_gemm_desc& d, int named) {
   }
   const std::uint64_t small_tiles = ((d.m + 127) / 128) * ((d.n + 127) / 128);
   const bool short_i8 = d.ab_type == CAIRN_TYPE_I8 && d.k > 0 && d.k <= 1024 && small_tiles <= std::uint64_t(CUS);
-  for(const int family : short_i8 ? std::initializer_list<int>{MFMA, WAVE} : std::initializer_list<int>{WAVE, MFMA})
+  // The 8-bit floats go to the MFMA kernel, which widens them to f16: the ring's 8-bit float matrix core adds its
+  // products with a narrower alignment than the contract allows (it runs only where named).
+  const auto order = float8(d.ab_type) ? std::initializer_list<int>{MFMA}
+                                       : (short_i8 ? std::initializer_list<int>{MFMA, WAVE}
+                                                   : std::initializer_list<int>{WAVE, MFMA});
+  for(const int family : order)
     for(int id = 1; id <= COUNT; ++id)
       if(TABLE[id - 1].family == family && tiled_fits(d, TABLE[id - 1])) return id;
   for(int id = 1; id <= COUNT; ++id)

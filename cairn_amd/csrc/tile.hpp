@@ -27,10 +27,19 @@ namespace cairn::tile {
 typedef std::uint32_t u32x4 __attribute__((vector_size(16)));
 typedef std::uint32_t u32x2 __attribute__((vector_size(8)));
 
-// One tile configuration. ES is the operand's element size in bytes (2: bf16/f16, 1: int8). A k-step is 128 bytes
-// of every operand row (8 chunks of 16 bytes); an MFMA consumes 32 bytes of k (2 chunks): 16 bf16 or 32 int8.
-template<int BM_, int BN_, int ES_> struct Shape {
-  static constexpr int BM = BM_, BN = BN_, ES = ES_;
+// How operands cross from global memory into LDS: as stored, or (the 8-bit floats) widened to f16 in registers
+// between their load and their LDS store, exactly (every value of either format is an f16 value), so that they meet
+// the f16 matrix core, as the reference widens them for its f16 tensor cores (src/cairn/runtime/cairn_tensor.hpp:
+// 123-135).
+constexpr int WIDEN_NONE = 0, WIDEN_E4M3 = 1, WIDEN_E5M2 = 2;
+
+// One tile configuration. ES is the operand's element size in LDS, in bytes (2: bf16/f16 and the widened 8-bit
+// floats, 1: int8); GS its size in global memory (1 for the widened 8-bit floats, else ES). A k-step is 128 bytes of
+// every operand row in LDS (8 chunks of 16 bytes); an MFMA consumes 32 bytes of k (2 chunks): 16 bf16 or 32 int8.
+template<int BM_, int BN_, int ES_, int W_ = WIDEN_NONE> struct Shape {
+  static constexpr int BM = BM_, BN = BN_, ES = ES_, W = W_;
+  static constexpr int GS = W_ == WIDEN_NONE ? ES_ : 1;
+  static_assert(W_ == WIDEN_NONE || ES_ == 2, "the 8-bit floats widen to f16");
   static constexpr int ROW = 128;              // bytes of one operand row per k-step, in LDS
   static constexpr int CHUNKS = ROW / 16;      // 8
   static constexpr int BK = ROW / ES;          // k elements per k-step: 64 or 128
@@ -101,6 +110,41 @@ CAIRN_HD void transpose_b8(const u32x2 in[16], u32x4 out[8]) {
       const std::uint32_t b2 = (in[4 * e + 2][w] >> s) & 0xffu, b3 = (in[4 * e + 3][w] >> s) & 0xffu;
       out[j][e] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
     }
+}
+
+// Eight 8-bit floats (byte e of the pair is element e) as eight f16 patterns (two to a word, the lower element in
+// the low half), exactly. E5M2 is the top byte of the f16 of the same value. E4M3 goes through the hardware's packed
+// conversion at scale 1 on the device (an f16 holds every E4M3 value, subnormals included) and through the same
+// rebias in integer steps on the host (the simulator), its NaN to f16's quiet NaN.
+CAIRN_HD std::uint16_t e4m3_as_f16(std::uint32_t x) {
+  const std::uint32_t sign = (x & 0x80u) << 8, e = (x >> 3) & 15u, f = x & 7u;
+  if(e == 15u && f == 7u) return std::uint16_t(sign | 0x7e00u);
+  if(e == 0u) {
+    if(f == 0u) return std::uint16_t(sign);
+    const unsigned lead = f >= 4u ? 2u : (f >= 2u ? 1u : 0u);  // f * 2^-9 = 1.xx * 2^(lead - 9)
+    return std::uint16_t(sign | ((lead + 6u) << 10) | ((f - (1u << lead)) << (10u - lead)));
+  }
+  return std::uint16_t(sign | ((e + 8u) << 10) | (f << 7));
+}
+template<int W> CAIRN_HD u32x4 widened(u32x2 raw) {
+  u32x4 out;
+#pragma unroll
+  for(int h = 0; h < 2; ++h) {
+    const std::uint32_t x = raw[h];
+    if constexpr(W == WIDEN_E5M2) {
+      out[2 * h] = ((x & 0xffu) << 8) | ((x & 0xff00u) << 16);
+      out[2 * h + 1] = ((x >> 8) & 0xff00u) | (x & 0xff000000u);
+    } else {
+#if defined(__HIP_DEVICE_COMPILE__)
+      out[2 * h] = __builtin_bit_cast(std::uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false));
+      out[2 * h + 1] = __builtin_bit_cast(std::uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true));
+#else
+      out[2 * h] = std::uint32_t(e4m3_as_f16(x & 0xffu)) | (std::uint32_t(e4m3_as_f16((x >> 8) & 0xffu)) << 16);
+      out[2 * h + 1] = std::uint32_t(e4m3_as_f16((x >> 16) & 0xffu)) | (std::uint32_t(e4m3_as_f16(x >> 24)) << 16);
+#endif
+    }
+  }
+  return out;
 }
 
 // The LDS chunk lane l reads for MFMA k-step s of the 32-row block starting at `row0`: row row0 + l%32, chunk
@@ -200,21 +244,23 @@ CAIRN_HD Panel panel(bool kmajor, int first, int total, int k, std::int64_t ld, 
 // Mem::Rsrc Mem::resource(const char* base, int64 bytes); Mem::load16(Rsrc, int) -> u32x4; Mem::load8 -> u32x2.
 template<class Sh, int R, bool KMAJOR, class Mem> struct Operand;
 
-// K-contiguous rows: slot u of thread t is row kmajor_slot(t,u).row, chunk .chunk; 16-byte loads.
+// K-contiguous rows: slot u of thread t is row kmajor_slot(t,u).row, chunk .chunk; 16-byte loads (8-byte ones of
+// the 8-bit floats that widen to a 16-byte chunk).
 template<class Sh, int R, class Mem> struct Operand<Sh, R, true, Mem> {
   static constexpr int SLOTS = R * Sh::CHUNKS / Sh::THREADS;
-  u32x4 v[SLOTS];
+  using Raw = typename std::conditional<Sh::GS == Sh::ES, u32x4, u32x2>::type;
+  Raw v[SLOTS];
   int offset[SLOTS];  // from the panel's start, or OUTSIDE for rows past `total`
   CAIRN_HD void setup(int t, int first, int total, std::int64_t ld) {
 #pragma unroll
     for(int u = 0; u < SLOTS; ++u) {
       const Slot s = kmajor_slot(t, u);
-      offset[u] = first + s.row < total ? int(s.row * ld * Sh::ES) + 16 * s.chunk : OUTSIDE;
+      offset[u] = first + s.row < total ? int(s.row * ld * Sh::GS) + Sh::CE * Sh::GS * s.chunk : OUTSIDE;
     }
   }
-  // k-step kt: the panel advanced by kt * 128 bytes; chunks at or past k read nothing.
+  // k-step kt: the panel advanced by kt * BK elements; chunks at or past k read nothing.
   CAIRN_HD void fetch(Mem& mem, const char* base, const Panel& p, std::int64_t, int kt, int k, int t) {
-    const std::int64_t step = std::int64_t(kt) * Sh::ROW;
+    const std::int64_t step = std::int64_t(kt) * Sh::BK * Sh::GS;
     const auto r = mem.resource(base + p.start + step, p.bytes - step);
     const int k0 = kt * Sh::BK;
     const bool tail = k0 + Sh::BK > k;
@@ -222,42 +268,45 @@ template<class Sh, int R, class Mem> struct Operand<Sh, R, true, Mem> {
     for(int u = 0; u < SLOTS; ++u) {
       int o = offset[u];
       if(tail && k0 + kmajor_slot(t, u).chunk * Sh::CE >= k) o = OUTSIDE;
-      v[u] = mem.load16(r, o);
+      if constexpr(Sh::GS == Sh::ES) v[u] = mem.load16(r, o);
+      else v[u] = mem.load8(r, o);
     }
   }
   template<class Lds> CAIRN_HD void store(Lds& lds, int stage, int t) const {
 #pragma unroll
     for(int u = 0; u < SLOTS; ++u) {
       const Slot s = kmajor_slot(t, u);
-      lds.write16(stage + lds_offset(s.row, s.chunk), v[u]);
+      if constexpr(Sh::GS == Sh::ES) lds.write16(stage + lds_offset(s.row, s.chunk), v[u]);
+      else lds.write16(stage + lds_offset(s.row, s.chunk), widened<Sh::W>(v[u]));
     }
   }
 };
 
-// M- or N-contiguous rows: this thread's block of KR k rows x 8 columns, transposed into 8 K-major chunks.
+// M- or N-contiguous rows: this thread's block of KR k rows x 8 columns, transposed into 8 K-major chunks (the 8-bit
+// floats that widen: each k row's 8 bytes widened to 8 f16, then transposed as 16-bit elements).
 template<class Sh, int R, class Mem> struct Operand<Sh, R, false, Mem> {
   static constexpr int KR = Sh::KR;
-  using Piece = typename std::conditional<Sh::ES == 2, u32x4, u32x2>::type;
+  using Piece = typename std::conditional<Sh::GS == 2, u32x4, u32x2>::type;
   Piece v[KR];
   int col;    // byte offset of this thread's 8 columns in a stored row, or OUTSIDE
   bool live;  // holds a block
   CAIRN_HD void setup(int t, int first, int total, std::int64_t) {
     const Block b = mnmajor_block<R>(t);
     live = b.live;
-    col = b.live && first + 8 * b.nb < total ? 8 * b.nb * Sh::ES : OUTSIDE;
+    col = b.live && first + 8 * b.nb < total ? 8 * b.nb * Sh::GS : OUTSIDE;
   }
   // k-step kt: the panel advanced by kt * BK stored rows; rows at or past k read nothing.
   CAIRN_HD void fetch(Mem& mem, const char* base, const Panel& p, std::int64_t ld, int kt, int k, int t) {
     if(!live) return;
     const int k0 = kt * Sh::BK;
-    const std::int64_t step = std::int64_t(k0) * ld * Sh::ES;
+    const std::int64_t step = std::int64_t(k0) * ld * Sh::GS;
     const auto r = mem.resource(base + p.start + step, p.bytes - step);
     const int kb = mnmajor_block<R>(t).kb;
 #pragma unroll
     for(int q = 0; q < KR; ++q) {
       const int row = kb * KR + q;
-      const int o = col == OUTSIDE || k0 + row >= k ? OUTSIDE : int(row * ld * Sh::ES) + col;
-      if constexpr(Sh::ES == 2) v[q] = mem.load16(r, o);
+      const int o = col == OUTSIDE || k0 + row >= k ? OUTSIDE : int(row * ld * Sh::GS) + col;
+      if constexpr(Sh::GS == 2) v[q] = mem.load16(r, o);
       else v[q] = mem.load8(r, o);
     }
   }
@@ -265,8 +314,16 @@ template<class Sh, int R, class Mem> struct Operand<Sh, R, false, Mem> {
     if(!live) return;
     const Block b = mnmajor_block<R>(t);
     u32x4 out[8];
-    if constexpr(Sh::ES == 2) transpose_b16(v, out);
-    else transpose_b8(v, out);
+    if constexpr(Sh::GS == 2) {
+      transpose_b16(v, out);
+    } else if constexpr(Sh::ES == 2) {
+      u32x4 wide[8];
+#pragma unroll
+      for(int q = 0; q < 8; ++q) wide[q] = widened<Sh::W>(v[q]);
+      transpose_b16(wide, out);
+    } else {
+      transpose_b8(v, out);
+    }
 #pragma unroll
     for(int j = 0; j < 8; ++j) lds.write16(stage + lds_offset(8 * b.nb + j, b.kb), out[j]);
   }

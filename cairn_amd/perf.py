@@ -72,7 +72,9 @@ def predict(desc: L.Desc, data: dict | None = None) -> dict:
         return {"ns": d["launch_ns"] + memory, "kernel": choice["name"], "bound": "device memory",
                 "memory_ns": memory, "hbm_share": share}  # fmt: skip
     rate = g["kernels"][choice["name"]]["frac"]
-    peak = d["flops"][PEAK_KEY[desc.ab_type]] * rate * choice["efficiency"]
+    # The MFMA family widens the 8-bit floats to f16: its rates are shares of the f16 peak.
+    widened = choice["family"] == "mfma" and desc.ab_type in (L.F8E4M3, L.F8E5M2)
+    peak = d["flops"]["tensor_f16" if widened else PEAK_KEY[desc.ab_type]] * rate * choice["efficiency"]
     compute = work / peak
     memory = moved / (d["dram_gbps"] * d["memory_efficiency"])
     return {"ns": d["launch_ns"] + max(memory, compute), "kernel": choice["name"],

@@ -9,10 +9,14 @@
 //   3. every output element is written exactly once, and none outside the matrix;
 //   4. the outputs equal the exact product (values chosen so every sum is exact), old values added.
 //
+// The widened 8-bit float shapes load 8 bytes of an operand where the others load 16 and widen them to f16 between
+// the load and the LDS store (the host side of tile.hpp's widened), so rules 1-4 hold their loads and tails too.
+//
 // The matrix-core model: lane l supplies row l%32 of its operand and 16 bytes of k (chunk 2s + l/32); the output of
 // register r of lane l is row 8(r/4) + 4(l/32) + r%4 of the first operand, column l%32 of the second. The GPU tests
 // check the model against the hardware; this program checks everything around it. Mirrors, in spirit, the
 // reference's host run of its device tile (tests/runtime/tensor_runtime.cpp).
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -138,20 +142,103 @@ template<int ES> void decode(const std::uint8_t* chunk, double* out) {
   }
 }
 
-template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k, int pad, int group) {
-  using Sh = Shape<BM, BN, ES>;
+// The 8-bit floats' values, from their fields (E4M3: bias 7, no infinities, S.1111.111 NaN; E5M2: bias 15, IEEE
+// specials), and f16's, for the widened shapes' LDS chunks.
+double f8_value(std::uint8_t x, int w) {
+  const int sign = x & 0x80 ? -1 : 1;
+  const int mbits = w == WIDEN_E4M3 ? 3 : 2, bias = w == WIDEN_E4M3 ? 7 : 15;
+  const int e = (x & 0x7f) >> mbits, f = x & ((1 << mbits) - 1);
+  if(w == WIDEN_E4M3 && e == 15 && f == 7) return std::nan("");
+  if(w == WIDEN_E5M2 && e == 31) return f ? std::nan("") : sign * INFINITY;
+  const double mant = e ? 1.0 + std::ldexp(double(f), -mbits) : std::ldexp(double(f), -mbits);
+  return sign * std::ldexp(mant, (e ? e : 1) - bias);
+}
+double f16_value(std::uint16_t h) {
+  const int sign = h & 0x8000 ? -1 : 1, e = (h >> 10) & 31, f = h & 1023;
+  if(e == 31) return f ? std::nan("") : sign * INFINITY;
+  return sign * std::ldexp(e ? 1.0 + std::ldexp(double(f), -10) : std::ldexp(double(f), -10), (e ? e : 1) - 15);
+}
+// An operand's element: its size in memory (GS) and in LDS (ES), its value in memory and in an LDS chunk. The widened
+// 8-bit floats draw from every finite E4M3 pattern and from E5M2's with exponents 6 .. 25 (2^-9 .. 1.75 2^10), ranges
+// whose products' sums over k of a few thousand are exact in a double.
+template<int ES, int W> struct Codec {
+  static constexpr int GS = W == WIDEN_NONE ? ES : 1;
+  static double value(const std::vector<std::uint8_t>& m, std::int64_t at) {
+    if constexpr(W == WIDEN_NONE) return value_of<ES>(m, at);
+    else return f8_value(m[at], W);
+  }
+  static void put(std::vector<std::uint8_t>& m, std::int64_t at, std::uint64_t h) {
+    if constexpr(W == WIDEN_NONE) {
+      ::put<ES>(m, at, h);
+    } else if constexpr(W == WIDEN_E4M3) {
+      std::uint8_t x = std::uint8_t(h % 254);
+      m[at] = x >= 0x7f ? std::uint8_t(x + 1) : x;  // 0x7f (NaN) skipped; 0xff never drawn
+    } else {
+      const std::uint8_t e = std::uint8_t(6 + (h >> 8) % 20), f = std::uint8_t(h & 3), sign = std::uint8_t(h & 4 ? 0x80 : 0);
+      m[at] = std::uint8_t(sign | (e << 2) | f);
+    }
+  }
+  static void chunk(const std::uint8_t* c, double* out) {
+    if constexpr(W == WIDEN_NONE) {
+      decode<ES>(c, out);
+    } else {
+      for(int e = 0; e < 8; ++e) {
+        std::uint16_t h;
+        std::memcpy(&h, c + 2 * e, 2);
+        out[e] = f16_value(h);
+      }
+    }
+  }
+};
+
+// The host widening (the simulator's stand-in for the hardware conversion) gives every pattern's own value: E4M3 and
+// E5M2 are f16 values, so the widened f16 must decode to the same number (NaN to a NaN).
+void widening_is_exact() {
+  for(int w : {WIDEN_E4M3, WIDEN_E5M2}) {
+    for(int x = 0; x < 256; ++x) {
+      const u32x2 raw{std::uint32_t(x) * 0x01010101u, std::uint32_t(x) * 0x01010101u};
+      const u32x4 out = w == WIDEN_E4M3 ? widened<WIDEN_E4M3>(raw) : widened<WIDEN_E5M2>(raw);
+      for(int e = 0; e < 8; ++e) {
+        const std::uint16_t h = std::uint16_t(out[e / 2] >> (16 * (e % 2)));
+        const double want = f8_value(std::uint8_t(x), w), got = f16_value(h);
+        if(std::isnan(want) ? !std::isnan(got) : (got != want || std::signbit(got) != std::signbit(want))) {
+          std::printf("widen %s 0x%02x: element %d is f16 0x%04x = %.9g, want %.9g\n", w == WIDEN_E4M3 ? "e4m3" : "e5m2",
+                      x, e, h, got, want);
+          ++failures;
+          return;
+        }
+      }
+    }
+    // Distinct bytes land in their own elements, in order.
+    const u32x2 ramp{0x43424140u, 0x47464544u};
+    const u32x4 r = w == WIDEN_E4M3 ? widened<WIDEN_E4M3>(ramp) : widened<WIDEN_E5M2>(ramp);
+    for(int e = 0; e < 8; ++e) {
+      const std::uint16_t h = std::uint16_t(r[e / 2] >> (16 * (e % 2)));
+      if(f16_value(h) != f8_value(std::uint8_t(0x40 + e), w)) {
+        std::printf("widen: element %d out of place\n", e);
+        ++failures;
+        return;
+      }
+    }
+  }
+}
+
+template<int BM, int BN, int ES, bool TA, bool TB, int W = WIDEN_NONE> void run(int m, int n, int k, int pad, int group) {
+  using Sh = Shape<BM, BN, ES, W>;
+  using V = Codec<ES, W>;
+  constexpr int GS = V::GS;
   constexpr bool AK = !TA, BK_ = TB;
   const char* lay = TA ? (TB ? "TT" : "TN") : (TB ? "NT" : "NN");
   // Stored matrices, padded: a is m x k (TA: k x m), b is k x n (TB: n x k).
   const std::int64_t lda = (TA ? m : k) + pad, ldb = (TB ? k : n) + pad, ldc = n + pad;
   const std::int64_t arows = TA ? k : m, brows = TB ? n : k;
-  const std::int64_t abytes = std::max<std::int64_t>(1, ((arows ? arows - 1 : 0) * lda + (TA ? m : k)) * ES);
-  const std::int64_t bbytes = std::max<std::int64_t>(1, ((brows ? brows - 1 : 0) * ldb + (TB ? k : n)) * ES);
+  const std::int64_t abytes = std::max<std::int64_t>(1, ((arows ? arows - 1 : 0) * lda + (TA ? m : k)) * GS);
+  const std::int64_t bbytes = std::max<std::int64_t>(1, ((brows ? brows - 1 : 0) * ldb + (TB ? k : n)) * GS);
   std::vector<std::uint8_t> A(abytes, 0x7f), B(bbytes, 0x7f);  // padding: 0x7f7f is a huge bf16, 127 an int8
   for(std::int64_t r = 0; r < arows; ++r)
-    for(int q = 0; q < (TA ? m : k); ++q) put<ES>(A, r * lda + q, mix(11 + r * 7919 + q));
+    for(int q = 0; q < (TA ? m : k); ++q) V::put(A, r * lda + q, mix(11 + r * 7919 + q));
   for(std::int64_t r = 0; r < brows; ++r)
-    for(int q = 0; q < (TB ? k : n); ++q) put<ES>(B, r * ldb + q, mix(23 + r * 104729 + q));
+    for(int q = 0; q < (TB ? k : n); ++q) V::put(B, r * ldb + q, mix(23 + r * 104729 + q));
   auto a_at = [&](int i, int p) { return TA ? std::int64_t(p) * lda + i : std::int64_t(i) * lda + p; };
   auto b_at = [&](int p, int j) { return TB ? std::int64_t(j) * ldb + p : std::int64_t(p) * ldb + j; };
 
@@ -169,7 +256,7 @@ template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k,
     if(tm < 0 || tm >= tiles_m || tn < 0 || tn >= tiles_n) FAIL("%s tile_of(%d) = (%d, %d) off the grid", lay, wg, tm, tn);
     ++seen[tm * tiles_n + tn];
     const int row0 = tm * BM, col0 = tn * BN;
-    const Panel pa = panel(AK, row0, m, k, lda, ES), pb = panel(BK_, col0, n, k, ldb, ES);
+    const Panel pa = panel(AK, row0, m, k, lda, GS), pb = panel(BK_, col0, n, k, ldb, GS);
     std::vector<Operand<Sh, BM, AK, HostMem>> fa(Sh::THREADS);
     std::vector<Operand<Sh, BN, BK_, HostMem>> fb(Sh::THREADS);
     for(int t = 0; t < Sh::THREADS; ++t) {
@@ -200,8 +287,8 @@ template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k,
               constexpr int CE = 16 / ES;
               for(int l = 0; l < 64; ++l) {
                 double pb_[16], qa_[16];
-                decode<ES>(&lds.bytes[Sh::A_BYTES + fragment_offset(wn * Sh::WTN + 32 * j, s, l)], pb_);
-                decode<ES>(&lds.bytes[fragment_offset(wm * Sh::WTM + 32 * i, s, l)], qa_);
+                V::chunk(&lds.bytes[Sh::A_BYTES + fragment_offset(wn * Sh::WTN + 32 * j, s, l)], pb_);
+                V::chunk(&lds.bytes[fragment_offset(wm * Sh::WTM + 32 * i, s, l)], qa_);
                 for(int e = 0; e < CE; ++e) {
                   P[l & 31][(l >> 5) * CE + e] = pb_[e];
                   Q[(l >> 5) * CE + e][l & 31] = qa_[e];
@@ -247,7 +334,7 @@ template<int BM, int BN, int ES, bool TA, bool TB> void run(int m, int n, int k,
     for(int j = 0; j < n; ++j) {
       double want = old[std::size_t(i) * ldc + j];
       double exact = 0;
-      for(int p = 0; p < k; ++p) exact += value_of<ES>(A, a_at(i, p)) * value_of<ES>(B, b_at(p, j));
+      for(int p = 0; p < k; ++p) exact += V::value(A, a_at(i, p)) * V::value(B, b_at(p, j));
       want += exact;
       const std::size_t at = std::size_t(i) * ldc + j;
       if(written[at] != 1) FAIL("%s %dx%d es=%d %dx%dx%d: output (%d,%d) written %d times", lay, BM, BN, ES, m, n, k, i, j, written[at]);
@@ -518,21 +605,22 @@ template<class Sh> void pipe_shapes() {
   }
 }
 
-template<int BM, int BN, int ES> void layouts(int m, int n, int k, int pad, int group) {
-  run<BM, BN, ES, false, false>(m, n, k, pad, group);
-  run<BM, BN, ES, false, true>(m, n, k, pad, group);
-  run<BM, BN, ES, true, false>(m, n, k, pad, group);
-  run<BM, BN, ES, true, true>(m, n, k, pad, group);
+template<int BM, int BN, int ES, int W> void layouts(int m, int n, int k, int pad, int group) {
+  run<BM, BN, ES, false, false, W>(m, n, k, pad, group);
+  run<BM, BN, ES, false, true, W>(m, n, k, pad, group);
+  run<BM, BN, ES, true, false, W>(m, n, k, pad, group);
+  run<BM, BN, ES, true, true, W>(m, n, k, pad, group);
 }
 
-template<int BM, int BN, int ES> void shapes() {
-  // m and n multiples of 8 (the MN-major fetch's 8-column pieces), k a multiple of the 16-byte chunk; tails in every
-  // direction against the tile and the k-step, padded and packed leading dimensions, one and several groups.
+template<int BM, int BN, int ES, int W = WIDEN_NONE> void shapes() {
+  // m and n multiples of 8 (the MN-major fetch's 8-column pieces), k a multiple of the 16-byte LDS chunk; tails in
+  // every direction against the tile and the k-step, padded (by 8: the widened 8-bit floats' 8-byte pieces) and
+  // packed leading dimensions, one and several groups.
   constexpr int CE = 16 / ES;
   const int list[][5] = {{8, 8, CE, 0, 4},           {64, 64, 4 * CE, 8, 4},      {BM, BN, 128 / ES, 0, 4},
                          {BM + 8, BN + 24, 3 * CE, 8, 1}, {2 * BM + 72, BN - 8, 200 / CE * CE, 16, 2},
                          {264, 3 * BN + 8, 19 * CE, 0, 4}};
-  for(auto& s : list) layouts<BM, BN, ES>(s[0], s[1], s[2], s[3], s[4]);
+  for(auto& s : list) layouts<BM, BN, ES, W>(s[0], s[1], s[2], s[3], s[4]);
 }
 
 }  // namespace
@@ -561,6 +649,9 @@ int main() {
   shapes<256, 256, 1>();
   shapes<256, 128, 1>();
   shapes<128, 128, 1>();
+  widening_is_exact();
+  shapes<128, 128, 2, WIDEN_E4M3>();
+  shapes<128, 128, 2, WIDEN_E5M2>();
   // tile_of is a bijection for grids whose size is and is not a multiple of 8, and for partial groups.
   for(int tm = 1; tm <= 13; ++tm)
     for(int tn = 1; tn <= 11; ++tn)

@@ -190,9 +190,16 @@ def test_the_selector_picks_a_kernel_for_every_baseline_config():
 
 def test_the_selector_falls_back_to_the_generic_kernel_where_chunks_do_not_fit():
     assert choose(L.BF16, L.F32, 65, 63, 33, P, P, P, accumulate=True)["family"] == "generic"  # k % 8
-    assert choose(L.F8E4M3, L.F32, 200, 136, 72, P, P, P, accumulate=True)["family"] == "generic"  # rows too short
-    f8 = choose(L.F8E5M2, L.F32, 256, 256, 256, P, P, P, accumulate=True)  # the fp8 matrix core, not widened
-    assert f8["family"] == "wave" and f8["name"] == "cairn_wave_f8e5m2_nn_256x256"
+    assert choose(L.F8E4M3, L.F32, 200, 136, 68, P, P, P, accumulate=True)["family"] == "generic"  # k % 8
+    assert choose(L.F8E4M3, L.F32, 200, 132, 72, P, P, P, accumulate=True)["family"] == "generic"  # n % 8 (NN's b)
+    # The 8-bit floats go to the MFMA kernel, which widens them to f16 (8-byte pieces: 72 of k is enough); the ring's
+    # 8-bit float matrix core runs where it is named.
+    assert choose(L.F8E4M3, L.F32, 200, 136, 72, P, P, P, accumulate=True)["name"] == "cairn_mfma_f8e4m3_nn_128x128"
+    f8 = choose(L.F8E5M2, L.F32, 256, 256, 256, P, P, P, accumulate=True)
+    assert f8["family"] == "mfma" and f8["name"] == "cairn_mfma_f8e5m2_nn_128x128" and f8["tile_k"] == 64
+    named = choose(L.F8E5M2, L.F32, 256, 256, 256, P, P, P, accumulate=True,
+                   kernel=L.kernel_named("cairn_wave_f8e5m2_nn_256x256"))  # fmt: skip
+    assert named["name"] == "cairn_wave_f8e5m2_nn_256x256"
     assert choose(L.BF16, L.F32, 256, 256, 256, P + 2, P, P)["family"] == "generic"  # a off 16 bytes
     assert choose(L.BF16, L.F32, 256, 250, 256, P, P, P)["family"] == "generic"  # n % 4
 

@@ -229,30 +229,103 @@ def test_random_operands_keep_the_contract_on_every_layout(fmt, trans_a, trans_b
         assert H.outside(v, exact, room) == 0
 
 
+def f8_patterns(rng, fmt: int, shape) -> np.ndarray:
+    """Every finite pattern of the 8-bit float at random, subnormals and the largest values included."""
+    p = rng.integers(0, 256, shape, dtype=np.uint8)
+    bad = ~np.isfinite(H.values(fmt, p))
+    while bad.any():
+        p[bad] = rng.integers(0, 256, int(bad.sum()), dtype=np.uint8)
+        bad = ~np.isfinite(H.values(fmt, p))
+    return p
+
+
 @pytest.mark.parametrize("trans_a,trans_b", LAYOUTS)
 @pytest.mark.parametrize("fmt", [L.F8E4M3, L.F8E5M2])
-def test_fp8_on_the_fp8_matrix_core_keeps_the_contract(fmt, trans_a, trans_b):
-    """The 8-bit floats on v_mfma_f32_32x32x64_f8f6f4 (not widened): every finite pattern of the format at random,
-    subnormals and the largest values included; products exact, the sum within the contract of its exact value."""
+def test_fp8_keeps_the_contract_on_every_layout(fmt, trans_a, trans_b):
+    """The 8-bit floats as the selector runs them (widened to f16 on their way into LDS, the f16 matrix core): random
+    patterns over the whole range, short k (where one large product and many small ones share a group of the matrix
+    core's adds) and long, products exact, each sum within the contract of its exact value."""
     rng = np.random.default_rng(8 + 4 * fmt + 2 * trans_a + trans_b)
+    for m, n, k in [(512, 768, 1024), (1536, 1040, 272), (264, 136, 16), (136, 264, 72)]:
+        a = f8_patterns(rng, fmt, (k, m) if trans_a else (m, k))
+        b = f8_patterns(rng, fmt, (n, k) if trans_b else (k, n))
+        A, B = H.values(fmt, a), H.values(fmt, b)
+        exact, mag = H.exact_product(A.T if trans_a else A, B.T if trans_b else B)
+        c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
+        got, ch = run_gemm(fmt, L.F32, m, n, k, a, b, c0, trans_a=trans_a, trans_b=trans_b, accumulate=True)
+        assert ch["name"].startswith("cairn_mfma_f8"), ch["name"]
+        assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0, (m, n, k)
+
+
+@pytest.mark.parametrize("trans_a,trans_b", LAYOUTS)
+@pytest.mark.parametrize("fmt", [L.F8E4M3, L.F8E5M2])
+def test_every_pattern_pair_of_the_8_bit_floats_multiplies_exactly(fmt, trans_a, trans_b):
+    """a's column 0 holds each of the 256 patterns once, b's row 0 each once (the rest of k zero): c[i, j] is the
+    product of patterns i and j, exact in f32 (its sign too, where it is not zero), NaN where either is NaN or an
+    infinity meets zero, so every pattern widens to its own value in both operands' loads (K- and M/N-contiguous)."""
+    m = n = 256
+    k = 8
+    pats = np.arange(256, dtype=np.uint8)
+    zero = np.uint8(0)
+    a = np.full((m, k), zero, dtype=np.uint8)
+    a[:, 0] = pats
+    b = np.full((k, n), zero, dtype=np.uint8)
+    b[0, :] = pats[::-1]
+    v = H.values(fmt, pats)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = v[:, None] * v[::-1][None, :]
+    got, ch = run_gemm(fmt, L.F32, m, n, k, np.ascontiguousarray(a.T) if trans_a else a,
+                       np.ascontiguousarray(b.T) if trans_b else b, trans_a=trans_a, trans_b=trans_b)  # fmt: skip
+    assert ch["name"].startswith("cairn_mfma_f8"), ch["name"]
+    g = got.astype(np.float64)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(g), nan)
+    assert np.array_equal(g[~nan], want[~nan])
+    # Signs of the nonzero results (a zero product's sign is lost to the +0 products of the rest of k: -0 + +0 = +0).
+    live = ~nan & (want != 0)
+    assert np.array_equal(np.signbit(g[live]), np.signbit(want[live]))
+
+
+@pytest.mark.parametrize("fmt", [L.F8E4M3, L.F8E5M2])
+def test_fp8_keeps_products_far_below_the_largest_in_its_group(fmt):
+    """One product of 2^8 and fifteen of 2^-6 in each 16 of k (2^7 and 2^-7 in odd columns): their sum is exact in
+    f32, and the selector's path returns it bit for bit. The 8-bit float matrix core (the ring's wave8 kernels, which
+    run only where named) adds such a group with a narrower alignment and loses part of the small terms."""
+    small = 2.0**-6
+    m, n, k = 256, 256, 64
+    A = np.full((m, k), small, dtype=np.float64)
+    A[:, ::16] = 16.0
+    B = np.ones((k, n), dtype=np.float64)
+    B[::16, :] = 16.0
+    B[:, 1::2] *= 0.5
+    a, b = H.encode(fmt, A.ravel()).reshape(m, k), H.encode(fmt, B.ravel()).reshape(k, n)
+    assert np.array_equal(H.values(fmt, a), A) and np.array_equal(H.values(fmt, b), B)
+    exact = A @ B
+    assert np.array_equal(exact.astype(np.float32).astype(np.float64), exact)
+    got, ch = run_gemm(fmt, L.F32, m, n, k, a, b)
+    assert ch["name"].startswith("cairn_mfma_f8"), ch["name"]
+    assert np.array_equal(got.astype(np.float64), exact)
+
+
+@pytest.mark.parametrize("fmt", [L.F8E4M3, L.F8E5M2])
+def test_the_fp8_matrix_core_kernels_at_long_k(fmt):
+    """The ring's 8-bit float kernels (v_mfma_f32_32x32x64_f8f6f4, not widened; run where named), every layout, at
+    k = 1024 on random patterns: there the contract's room, (k + 1) 2^-22 sum |a b|, holds what their grouped adds
+    lose. (At short k it does not: the selector's path widens instead.)"""
+    rng = np.random.default_rng(18 + fmt)
     m, n, k = 512, 768, 1024
-
-    def patterns(shape):
-        p = rng.integers(0, 256, shape, dtype=np.uint8)
-        bad = ~np.isfinite(H.values(fmt, p))
-        while bad.any():
-            p[bad] = rng.integers(0, 256, int(bad.sum()), dtype=np.uint8)
-            bad = ~np.isfinite(H.values(fmt, p))
-        return p
-
-    a = patterns((k, m) if trans_a else (m, k))
-    b = patterns((n, k) if trans_b else (k, n))
-    A, B = H.values(fmt, a), H.values(fmt, b)
-    exact, mag = H.exact_product(A.T if trans_a else A, B.T if trans_b else B)
-    c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
-    got, ch = run_gemm(fmt, L.F32, m, n, k, a, b, c0, trans_a=trans_a, trans_b=trans_b, accumulate=True)
-    assert ch["name"].startswith("cairn_wave_f8"), ch["name"]
-    assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
+    for ta, tb in LAYOUTS:
+        lay = ("t" if ta else "n") + ("t" if tb else "n")
+        a = f8_patterns(rng, fmt, (k, m) if ta else (m, k))
+        b = f8_patterns(rng, fmt, (n, k) if tb else (k, n))
+        A, B = H.values(fmt, a), H.values(fmt, b)
+        exact, mag = H.exact_product(A.T if ta else A, B.T if tb else B)
+        c0 = rng.uniform(-4, 4, (m, n)).astype(np.float32)
+        name = f"cairn_wave_{L.TYPE_NAMES[fmt].lower()}_{lay}_256x256"
+        got, ch = run_gemm(fmt, L.F32, m, n, k, a, b, c0, trans_a=ta, trans_b=tb, accumulate=True,
+                           kernel=L.kernel_named(name))  # fmt: skip
+        assert ch["name"] == name
+        assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0, name
 
 
 def test_two_runs_give_the_same_bits():

@@ -71,10 +71,14 @@ def test_the_prediction_prices_the_kernel_the_selector_launches():
     ragged = perf.predict(L.desc(L.BF16, L.BF16, 520, n, n, P, P, P), data)
     assert ragged["tiling_efficiency"] < 0.2 and ragged["compute_ns"] > 4.0 * 2.0 * 520 * n * n / (
         d["flops"]["tensor_bf16"] * rate)
-    # fp8 at the fp8 peak on its own kernel; int8 at the int8 peak.
+    # fp8 as the selector runs it (widened to f16) at the f16 peak; on the fp8 matrix core (named) at the fp8 peak.
     f8 = perf.predict(L.desc(L.F8E4M3, L.BF16, n, n, n, P, P, P), data)
-    assert f8["kernel"].startswith("cairn_wave_f8e4m3") and math.isclose(
-        f8["compute_ns"], 2.0 * n**3 / (d["flops"]["tensor_f8"] * g["kernels"][f8["kernel"]]["frac"]), rel_tol=1e-9)
+    assert f8["kernel"].startswith("cairn_mfma_f8e4m3") and math.isclose(
+        f8["compute_ns"], 2.0 * n**3 / (d["flops"]["tensor_f16"] * g["kernels"][f8["kernel"]]["frac"]), rel_tol=1e-9)
+    core = L.desc(L.F8E4M3, L.BF16, n, n, n, P, P, P, kernel=L.kernel_named("cairn_wave_f8e4m3_nn_256x256"))
+    f8c = perf.predict(core, data)
+    assert f8c["kernel"] == "cairn_wave_f8e4m3_nn_256x256" and math.isclose(
+        f8c["compute_ns"], 2.0 * n**3 / (d["flops"]["tensor_f8"] * g["kernels"][f8c["kernel"]]["frac"]), rel_tol=1e-9)
     # The decode shape: the skinny kernel at its measured share of HBM.
     dec = perf.predict(L.desc(L.BF16, L.BF16, 1, 14336, 4096, P, P, P, trans_b=True), data)
     moved = (4096 + 14336 * 4096) * 2 + 14336 * 2
