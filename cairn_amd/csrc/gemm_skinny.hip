@@ -135,9 +135,9 @@ __global__ void __launch_bounds__(64 * WAVES) skinny_gemm(Params p, int width) {
   }
 }
 
-// The ring form, for m > 4 and n >= 8192 (workgroups of 64 columns, at least 128 of them): b's 64 rows and a's
-// 16 rows go from HBM straight into an LDS ring by `buffer_load ... lds`, KC bytes of k a row a stage, S stages, so
-// that up to S - 1 stages (3 x 40 KiB a CU) are in flight without a register held for them, each load 2 rows x 512
+// The ring form (cairn_skinny says for which m and n, with which stages and widths): b's rows of the workgroup (up to
+// 64) and a's 16 rows go from HBM straight into an LDS ring by `buffer_load ... lds`, KC bytes of k a row a stage, S
+// stages, so that up to S - 1 stages are in flight without a register held for them, each load 1024 / KC rows x KC
 // contiguous bytes. Wave w multiplies rows 16 w .. 16 w + 15 of b (the workgroup's columns) over the whole stage, so
 // its accumulator is whole at the end and nothing is reduced across waves. One barrier a stage, as the GEMM ring
 // (wave.hpp): past it the stage has landed for every wave and the stage before it is free for the refill.
@@ -237,18 +237,19 @@ __global__ void __launch_bounds__(256) skinny_ring(Params p, int width) {
 }
 
 // The row-streaming form, for m = 1 and k <= 4096 (a decode step's one token): a wave owns a contiguous
-// run of b's rows (the output's columns) and reads each row front to back, 1 KiB a load (64 lanes x 16 bytes), so
+// run of b's rows (the output's columns), wave w of `waves` rows [w n / waves, (w + 1) n / waves), so that no two
+// waves' runs differ by more than a row, and reads each row front to back, 1 KiB a load (64 lanes x 16 bytes), so
 // every wave streams one contiguous region of HBM, as a plain copy does. The arithmetic is small enough for the
 // vector ALUs: lane l holds a's 16-byte pieces at the same k as its pieces of b (loaded once), multiplies and adds
 // in f32 (every product of two bf16 exact, each sum one rounding: the contract), and the wave's 64 partial sums of a
 // row meet in a fixed DPP pattern, so two runs give the same bits. The next row's loads are issued before the
 // current row is summed: two rows of a wave in flight, KCH KiB each.
 template<int M, int KCH>
-__global__ void __launch_bounds__(256) skinny_rows(Params p, int per_wave) {
+__global__ void __launch_bounds__(256) skinny_rows(Params p, int waves) {
   const int t = threadIdx.x, lane = t & 63;
   const int wave = int(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(t >> 6);
-  const int first = wave * per_wave;
-  const int last = first + per_wave < p.n ? first + per_wave : p.n;  // rows [first, last) of b
+  const int first = int(std::int64_t(wave) * p.n / waves);
+  const int last = int(std::int64_t(wave + 1) * p.n / waves);  // rows [first, last) of b
   if(first >= last) return;
   const int kbytes = p.k * 2;
   // Piece c of a row: bytes 1024 c + 16 l; past k it reads zeros.
@@ -423,12 +424,26 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 4096, the LDS ring
   // (4.6 against 4.4 TB/s for the register form at m = 16, and 4.0 for the streaming form, whose loads of a's 16
   // rows double the L2 traffic); otherwise the register form.
-  // Whole rows a wave: 8 waves a CU, 12 from n = 12288 (side by side at n = 14336, k = 4096: 5.41 TB/s against 5.30
-  // for 8 a CU, 5.35 for 4 and 5.39 for 16; below n = 12288 8 a CU was fastest at every shape tried).
-  const int row_waves = p.n >= 12288 ? 3072 : 2048;
-  const int per_wave = (p.n + row_waves - 1) / row_waves;
-  if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(per_wave) * p.ldb * 2 < 0x7f000000LL) {
-    hipLaunchKernelGGL((cairn::gemm::skinny_rows<1, 8>), dim3(unsigned(row_waves / 4)), dim3(256), 0, s, p, per_wave);
+  // Whole rows a wave, dealt evenly: 8 waves a CU, 16 (the most its registers allow) from n = 12288. Side by side at
+  // n = 14336, k = 4096: 5.56 TB/s for 16 a CU, against 5.39 for 12 and 8 a CU dealt evenly, and 5.35 for the earlier
+  // rule of ceil(n / waves) rows a wave, which left a fifth of the CUs with two thirds of the rows of the others.
+  const int row_waves = p.n >= 12288 ? 4096 : 2048;
+  const int most = (p.n + row_waves - 1) / row_waves;  // rows the busiest wave streams
+  if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(most) * p.ldb * 2 < 0x7f000000LL) {
+    hipLaunchKernelGGL((cairn::gemm::skinny_rows<1, 8>), dim3(unsigned(row_waves / 4)), dim3(256), 0, s, p, row_waves);
+    return hipGetLastError();
+  }
+  // The ring with three 512-byte stages (120 KiB of LDS, one workgroup a CU), n spread evenly over the CUs, where that
+  // gives 48 or 56 columns a workgroup (n = 10241 .. 14336: one round of at most 256 workgroups), and for m > 4 at 64
+  // columns up to n = 16384. A load brings two rows' 512 contiguous bytes instead of four rows' 256. Side by side over
+  // n = 4096 .. 28672 and m = 2, 4, 8, 16 (k = 4096) against the forms below: at n = 14336 5.0-5.05 TB/s against
+  // 4.70-4.85 (m = 2 .. 16), at n = 11008 4.79-4.90 against 4.44-4.69, at n = 16384 and m >= 8 4.63-4.71 against
+  // 4.45; at 64 columns and m <= 4, below n = 10240 and past 16384 (two 80 KiB workgroups a CU) they were as fast or
+  // faster. Four 512-byte stages, five or more 256-byte ones, and two 1 KiB ones were all slower at n = 14336.
+  const int even = cairn_skinny_width(p.n);
+  if(p.m >= 2 && ((even >= 48 && even <= 56) || (p.m > 4 && even == 64 && p.n <= 256 * 64))) {
+    hipLaunchKernelGGL((cairn::gemm::skinny_ring<3, 512>), dim3(unsigned((p.n + even - 1) / even)), dim3(256), 0, s,
+                       p, even);
     return hipGetLastError();
   }
   if(p.m >= 2 && p.m <= 4 && p.n >= 2048) {  // rows of b a workgroup: n over the 256 CUs, 16 .. 64
@@ -449,7 +464,6 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
     // faster at n = 5120 .. 7168, even at 14336 (4.8 TB/s either way at 56 columns), 2-4% faster at 8192 and 2-15%
     // from 16384 on, where two workgroups a CU keep every CU streaming. 32 columns where they give 257 .. 511
     // workgroups (n = 10240 .. 14336) measured far slower.
-    const int even = cairn_skinny_width(p.n);
     const int width = p.n < 8192 ? 32 : (even >= 56 ? even : 64);
     hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 256>), dim3(unsigned((p.n + width - 1) / width)), dim3(256), 0, s,
                        p, width);

@@ -419,16 +419,19 @@ def test_skinny_decode_shapes_keep_the_contract(m):
     assert H.outside(v, exact, room) == 0
 
 
-# m > 4 with n >= 4096 takes the ring form (256-byte stages of k; 32 columns a workgroup below n = 8192, 56 or 64
-# above, two workgroups a CU past 256 of them), m = 1 with n >= 2048 and k <= 4096 the row-streaming one (whole rows
-# of b a wave), m = 2 .. 4 with n >= 2048 the streaming MFMA form (16 rows of b a wave; whole groups of 8 steps, then
+# m >= 2 with n spread over the CUs at 48 or 56 columns (n = 10241 .. 14336), and m > 4 at 64 columns up to n = 16384,
+# take the ring form with 512-byte stages; other m > 4 with n >= 4096 the ring form with 256-byte stages (32 columns a
+# workgroup below n = 8192, 64 above, two workgroups a CU past 256 of them), m = 1 with n >= 2048 and k <= 4096 the row-streaming one (whole rows
+# of b a wave, dealt evenly: a wave's share differs from the next one's by at most a row), m = 2 .. 4 with n >= 2048 the streaming MFMA form (16 rows of b a wave; whole groups of 8 steps, then
 # single steps, the last one partial), the rest the register form: tails in each.
 @pytest.mark.parametrize("m,n,k", [(1, 8, 8), (3, 100, 72), (16, 33, 4104), (7, 14336, 24), (5, 200, 4160),
                                    (2, 72, 1000), (3, 8200, 4104), (16, 9000, 520), (1, 8192, 8), (9, 8257, 1032),
                                    (1, 4100, 4096), (1, 3000, 1000), (1, 20000, 264), (1, 2048, 4088), (5, 8256, 4096),
                                    (2, 2048, 8), (4, 3001, 1000), (2, 70001, 40), (4, 2050, 520), (3, 14336, 4096),
                                    (8, 4096, 1000), (11, 6150, 264), (6, 20003, 520), (16, 28672, 136),
-                                   (5, 4095, 256)])
+                                   (5, 4095, 256), (1, 14336, 4096), (1, 12289, 1000), (1, 12288, 520),
+                                   (2, 11008, 4104), (4, 10241, 4096), (9, 12289, 24), (16, 16384, 520),
+                                   (5, 14336, 1000)])
 def test_skinny_tails_keep_the_contract(m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = H.normal_bf16(rng, (m, k), 1.0)
@@ -442,11 +445,12 @@ def test_skinny_tails_keep_the_contract(m, n, k):
 
 @pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_RELU])
 def test_every_skinny_form_applies_the_epilogue_in_its_stated_order(act):
-    """Row and column scales, a bf16 bias and an activation on each of the four skinny forms, bf16 out: equal, bit for
-    bit, to the stated steps applied in f32 to what the same form computes without them:
-    bf16(act((f32(acc) * rs[i]) * cs[j] + bias[j]))."""
+    """Row and column scales, a bf16 bias and an activation on each skinny form (the ring at both of its stage
+    sizes), bf16 out: equal, bit for bit, to the stated steps applied in f32 to what the same form computes without
+    them: bf16(act((f32(acc) * rs[i]) * cs[j] + bias[j]))."""
     rng = np.random.default_rng(31 + act)
-    for m, n, k in [(1, 4100, 1024), (3, 4100, 1000), (6, 8256, 512), (3, 200, 256)]:  # rows, stream, ring, register
+    # rows, stream, ring (256-byte stages), register, ring (512-byte stages)
+    for m, n, k in [(1, 4100, 1024), (3, 4100, 1000), (6, 8256, 512), (3, 200, 256), (6, 14336, 520)]:
         a = H.normal_bf16(rng, (m, k), 1.0)
         b = H.normal_bf16(rng, (n, k), 1.0)
         rs = rng.uniform(0.25, 2.0, m).astype(np.float32)

@@ -63,7 +63,8 @@ CASES = [
     ("C4 int8 W8A8 4096^3", L.I8, L.BF16, 4096, 4096, 4096, "nn", {"scales": True}, (0.85, 1.3)),
     ("C3 forward + bias + GELU", L.BF16, L.BF16, 8192, 11008, 4096, "nn", {"bias": True, "gelu": True}, (0.85, 1.35)),
     ("C3 dX (NT)", L.BF16, L.BF16, 8192, 4096, 11008, "nt", {}, (0.85, 1.3)),
-    ("C3 dW (TN)", L.BF16, L.BF16, 4096, 11008, 8192, "tn", {}, (0.85, 1.3)),
+    # 688 tiles: 2.69 rounds, the last a partial one the model charges as a full round at the full-load clock.
+    ("C3 dW (TN)", L.BF16, L.BF16, 4096, 11008, 8192, "tn", {}, (0.75, 1.3)),
     ("2048^3 (64 tiles)", L.BF16, L.BF16, 2048, 2048, 2048, "nn", {}, (0.55, 1.05)),
     ("520 x 4096 x 4096 (48 tiles)", L.BF16, L.BF16, 520, 4096, 4096, "nn", {}, (0.55, 1.05)),
     ("C5 decode m=1", L.BF16, L.BF16, 1, 14336, 4096, "nt", {}, (0.8, 1.2)),

@@ -154,7 +154,10 @@ def test_the_other_operand_types_split_too(fmt):
         return p
 
     a, b = operand((m, k)), operand((k, n))
-    got, ch = gemm(fmt, L.F32, m, n, k, a, b, split=True)
+    # The selector widens the 8-bit floats into the 128 x 128 kernel, which never splits: the ring's kernel on the fp8
+    # matrix core is named (at this k its grouped adds stay within the contract).
+    kernel = {"kernel": L.kernel_named("cairn_wave_f8e4m3_nn_256x256")} if fmt == L.F8E4M3 else {}
+    got, ch = gemm(fmt, L.F32, m, n, k, a, b, split=True, **kernel)
     assert ch["split_tiles"] == 8
     rows = np.nonzero(split_mask(m, n, 8).any(axis=1))[0][::4]
     exact, mag = H.exact_product(H.values(fmt, a[rows]), H.values(fmt, b))
