@@ -244,8 +244,8 @@ __global__ void __launch_bounds__(256) skinny_ring(Params p, int width) {
 // in f32 (every product of two bf16 exact, each sum one rounding: the contract), and the wave's 64 partial sums of a
 // row meet in a fixed DPP pattern, so two runs give the same bits. The next row's loads are issued before the
 // current row is summed: two rows of a wave in flight, KCH KiB each.
-template<int M, int KCH>
-__global__ void __launch_bounds__(256) skinny_rows(Params p, int waves) {
+template<int M, int KCH, bool PLAIN, int OUT>
+__global__ void __launch_bounds__(256, 3) skinny_rows(Params p, int waves) {
   const int t = threadIdx.x, lane = t & 63;
   const int wave = int(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(t >> 6);
   const int first = int(std::int64_t(wave) * p.n / waves);
@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(256) skinny_rows(Params p, int waves) {
   const char* brow = static_cast<const char*>(p.b) + std::int64_t(first) * p.ldb * 2;
   const __amdgpu_buffer_rsrc_t rb = span(brow, (std::int64_t(last - first - 1) * p.ldb + p.k) * 2);
   w32x4 xb[2][KCH];
-  auto load = [&](int r, w32x4 (&dst)[KCH]) {  // row first + r
+  auto load = [&](int r, w32x4 (&dst)[KCH]) {  // row first + r; past the wave's last row, zeros
 #pragma unroll
     for(int c = 0; c < KCH; ++c) {
       const int o = at(c);
@@ -286,7 +286,42 @@ __global__ void __launch_bounds__(256) skinny_rows(Params p, int waves) {
     const float s3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
     return (s0 + s1) + (s2 + s3);
   };
-  auto row = [&](int r, const w32x4 (&xr)[KCH]) {
+  // The epilogue's terms of row first + r (column n of the output), where there are any (PLAIN: none, and c is not
+  // read): its column scale and bias, and, for an f32 output accumulated into, the old values of c; identities (1, -0)
+  // where a term is absent, which change no bit of what the stated steps give. They are fetched with the row's own
+  // loads, through buffer ranges from the wave's first row (an absent term's range is empty and reads zero without
+  // touching memory), so that waiting for them is waiting for the row: loaded where the epilogue needs them, after
+  // the next row's loads, each wait for them would drain the prefetch (loads complete in order).
+  struct Terms {
+    std::uint32_t cs, b16, b32, old[M];
+  };
+  float rs[M];
+#pragma unroll
+  for(int i = 0; i < M; ++i) rs[i] = !PLAIN && p.row_scale && i < p.m ? p.row_scale[i] : 1.0f;
+  const int rows = last - first;
+  const bool old_c = OUT == CAIRN_TYPE_F32 && p.accumulate;
+  const bool bias16 = p.bias && p.bias_type == CAIRN_TYPE_BF16, bias32 = p.bias && !bias16;
+  auto range = [&](bool on, const void* base, int bytes) {
+    return span(on ? base : nullptr, on ? std::int64_t(rows) * bytes : 0);
+  };
+  const __amdgpu_buffer_rsrc_t r_cs = range(!PLAIN && p.col_scale, p.col_scale + first, 4);
+  const __amdgpu_buffer_rsrc_t r_b16 = range(!PLAIN && bias16, static_cast<const std::uint16_t*>(p.bias) + first, 2);
+  const __amdgpu_buffer_rsrc_t r_b32 = range(!PLAIN && bias32, static_cast<const float*>(p.bias) + first, 4);
+  __amdgpu_buffer_rsrc_t r_old[M];
+#pragma unroll
+  for(int i = 0; i < M; ++i)
+    r_old[i] = range(!PLAIN && old_c && i < p.m, static_cast<const float*>(p.c) + std::int64_t(i) * p.ldc + first, 4);
+  auto terms_of = [&](int r, Terms& v) {
+    if constexpr(!PLAIN) {
+      v.cs = __builtin_amdgcn_raw_buffer_load_b32(r_cs, 4 * r, 0, 0);
+      v.b16 = __builtin_amdgcn_raw_buffer_load_b16(r_b16, 2 * r, 0, 0);
+      v.b32 = __builtin_amdgcn_raw_buffer_load_b32(r_b32, 4 * r, 0, 0);
+#pragma unroll
+      for(int i = 0; i < M; ++i) v.old[i] = __builtin_amdgcn_raw_buffer_load_b32(r_old[i], 4 * r, 0, 0);
+    }
+  };
+  // Row first + r: its sums, then the epilogue's steps in their stated order (kernels.hpp, epilogue) and the store.
+  auto row = [&](int r, const w32x4 (&xr)[KCH], const Terms& tr) {
     float acc[M];
 #pragma unroll
     for(int i = 0; i < M; ++i) acc[i] = 0.0f;
@@ -306,28 +341,47 @@ __global__ void __launch_bounds__(256) skinny_rows(Params p, int waves) {
     const int n = first + r;
 #pragma unroll
     for(int i = 0; i < M; ++i) {
-      float v[1] = {wave_sum(acc[i])};
+      float v = wave_sum(acc[i]);
       if(i >= p.m || lane != 0) continue;
-      epilogue<1>(p, i, n, v);
-      const std::int64_t o = std::int64_t(i) * p.ldc + n;
-      if(p.c_type == CAIRN_TYPE_F32) {
-        float* out = static_cast<float*>(p.c) + o;
-        *out = p.accumulate ? *out + v[0] : v[0];
-      } else {
-        static_cast<std::uint16_t*>(p.c)[o] = p.c_type == CAIRN_TYPE_BF16 ? narrow_bf16(v[0]) : narrow_f16(v[0]);
+      if constexpr(!PLAIN) {
+        v = v * rs[i];
+        v = v * (p.col_scale ? from_bits(tr.cs) : 1.0f);
+        v = v + (bias16 ? from_bits(std::uint32_t(tr.b16) << 16) : (bias32 ? from_bits(tr.b32) : -0.0f));
+        if(p.act == CAIRN_ACT_RELU) v = v < 0.0f ? 0.0f : v;
+        else if(p.act == CAIRN_ACT_GELU) v = gelu(v);
       }
+      const std::int64_t o = std::int64_t(i) * p.ldc + n;  // OUT is the output's type: no branch on it a row
+      if constexpr(OUT == CAIRN_TYPE_F32) static_cast<float*>(p.c)[o] = !PLAIN && old_c ? from_bits(tr.old[i]) + v : v;
+      else if constexpr(OUT == CAIRN_TYPE_BF16) static_cast<std::uint16_t*>(p.c)[o] = narrow_bf16(v);
+      else static_cast<std::uint16_t*>(p.c)[o] = narrow_f16(v);
     }
   };
-  const int rows = last - first;
+  // Two rows an iteration, so that each buffer is named at compile time; the next row's loads (and terms) go out
+  // before a row is summed. Every iteration issues the loads of the row after its two, also past the wave's last
+  // row, where they read zeros without touching memory: issued on one path of a branch, they would leave the wait
+  // before the second row counting as if they had not been, a wait for that prefetch (measured 1-2% slower).
+  Terms t0, t1;
+  terms_of(0, t0);
   load(0, xb[0]);
   int r = 0;
-  for(; r + 2 <= rows; r += 2) {  // two rows an iteration, so that each buffer is named at compile time
+  for(; r + 2 <= rows; r += 2) {
+    terms_of(r + 1, t1);
     load(r + 1, xb[1]);
-    row(r, xb[0]);
-    if(r + 2 < rows) load(r + 2, xb[0]);
-    row(r + 1, xb[1]);
+    row(r, xb[0], t0);
+    terms_of(r + 2, t0);
+    load(r + 2, xb[0]);
+    row(r + 1, xb[1], t1);
   }
-  if(r < rows) row(r, xb[0]);
+  if(r < rows) row(r, xb[0], t0);
+}
+
+// The row-streaming form's launch: its instance for the epilogue (PLAIN: no terms, c not read) and output type.
+template<bool PLAIN> hipError_t launch_rows(const Params& p, hipStream_t s, int waves) {
+  const dim3 grid(unsigned(waves / 4)), block(256);
+  if(p.c_type == CAIRN_TYPE_BF16) hipLaunchKernelGGL((skinny_rows<1, 8, PLAIN, CAIRN_TYPE_BF16>), grid, block, 0, s, p, waves);
+  else if(p.c_type == CAIRN_TYPE_F16) hipLaunchKernelGGL((skinny_rows<1, 8, PLAIN, CAIRN_TYPE_F16>), grid, block, 0, s, p, waves);
+  else hipLaunchKernelGGL((skinny_rows<1, 8, PLAIN, CAIRN_TYPE_F32>), grid, block, 0, s, p, waves);
+  return hipGetLastError();
 }
 
 
@@ -424,14 +478,15 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 4096, the LDS ring
   // (4.6 against 4.4 TB/s for the register form at m = 16, and 4.0 for the streaming form, whose loads of a's 16
   // rows double the L2 traffic); otherwise the register form.
-  // Whole rows a wave, dealt evenly: 8 waves a CU, 16 (the most its registers allow) from n = 12288. Side by side at
-  // n = 14336, k = 4096: 5.56 TB/s for 16 a CU, against 5.39 for 12 and 8 a CU dealt evenly, and 5.35 for the earlier
-  // rule of ceil(n / waves) rows a wave, which left a fifth of the CUs with two thirds of the rows of the others.
-  const int row_waves = p.n >= 12288 ? 4096 : 2048;
+  // Whole rows a wave, dealt evenly: 8192 waves from n = 12288, 4096 from n = 4096, else 2048 (at most 12 of them a CU
+  // at once: 168 registers). Side by side at k = 4096 (TB/s): n = 14336 5.74 for 8192 waves, 5.64 for 4096, 5.50 for
+  // 2048; n = 12288 5.74, 5.62, 5.41; n = 8192 5.74, 5.83, 5.59; n = 4096 even.
+  const int row_waves = p.n >= 12288 ? 8192 : (p.n >= 4096 ? 4096 : 2048);
   const int most = (p.n + row_waves - 1) / row_waves;  // rows the busiest wave streams
-  if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(most) * p.ldb * 2 < 0x7f000000LL) {
-    hipLaunchKernelGGL((cairn::gemm::skinny_rows<1, 8>), dim3(unsigned(row_waves / 4)), dim3(256), 0, s, p, row_waves);
-    return hipGetLastError();
+  if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(most + 1) * p.ldb * 2 < 0x7f000000LL) {
+    const bool plain = !p.row_scale && !p.col_scale && !p.bias && p.act == CAIRN_ACT_NONE &&
+                       !(p.c_type == CAIRN_TYPE_F32 && p.accumulate);
+    return plain ? cairn::gemm::launch_rows<true>(p, s, row_waves) : cairn::gemm::launch_rows<false>(p, s, row_waves);
   }
   // The ring with three 512-byte stages (120 KiB of LDS, one workgroup a CU), n spread evenly over the CUs, where that
   // gives 48 or 56 columns a workgroup (n = 10241 .. 14336: one round of at most 256 workgroups), and for m > 4 at 64

@@ -443,6 +443,22 @@ def test_skinny_tails_keep_the_contract(m, n, k):
     assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
 
 
+@pytest.mark.parametrize("n", [2048, 4100, 12289, 14336])
+def test_the_row_streaming_form_rounds_its_own_f32_result_to_each_output_type(n):
+    """m = 1 (the row-streaming form, an instance per output type): bf16 and f16 outputs without an epilogue are, bit
+    for bit, the same form's f32 result rounded to nearest even."""
+    rng = np.random.default_rng(n)
+    k = 1000
+    a = H.normal_bf16(rng, (1, k), 1.0)
+    b = H.normal_bf16(rng, (n, k), 1.0)
+    raw, ch = run_gemm(L.BF16, L.F32, 1, n, k, a, b, trans_b=True)
+    assert ch["family"] == "skinny"
+    got_bf16, _ = run_gemm(L.BF16, L.BF16, 1, n, k, a, b, trans_b=True)
+    got_f16, _ = run_gemm(L.BF16, L.F16, 1, n, k, a, b, trans_b=True)
+    assert np.array_equal(got_bf16, H.bf16_from_f32(raw))
+    assert np.array_equal(got_f16, H.narrow_array(H.F16, raw))
+
+
 @pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_RELU])
 def test_every_skinny_form_applies_the_epilogue_in_its_stated_order(act):
     """Row and column scales, a bf16 bias and an activation on each skinny form (the ring at both of its stage
