@@ -457,6 +457,87 @@ def bench_ceiling(stream, steps: int, warmup: int, iterations: int = 8192) -> di
     return result
 
 
+STAMPS = ROOT / "tests" / "cpp" / "libwave_stamps.so"
+
+
+def bench_stamps(stream, steps: int, warmup: int, records: int = 8) -> dict:
+    """Where a one-round launch's time goes (tests/cpp/wave_stamps.hip: the ring kernel stamped at five points of each
+    wave's tile): C2 (bf16 4096^3) and C4 (int8 W8A8 4096^3). After the warm-up and a timed burst, `records` more
+    launches back to back, each stamping into its own record; for each, times in us from the launch's first stamp:
+    the first MFMA, the end of the main loop, the stores issued and done (min, median, max over the 1024 waves), the
+    XCDs' clocks and ends, the main loop's shader cycles a stage, and the gap from a launch's last store to the next
+    launch's first stamp. The figures of the median launch (by its last store) are returned."""
+    if not STAMPS.exists():
+        raise SystemExit(f"{STAMPS} is not built: run __graft_entry__.build()")
+    lib = C.CDLL(str(STAMPS))
+    vp = C.c_void_p
+    lib.wave_stamps_bf16.restype = lib.wave_stamps_i8.restype = C.c_int
+    lib.wave_stamps_bf16.argtypes = [vp, vp, vp, vp, C.c_int, vp]
+    lib.wave_stamps_i8.argtypes = [vp, vp, vp, vp, vp, vp, C.c_int, vp]
+    n, rng = 4096, np.random.default_rng(20261201)
+    tiles = (n // 256) ** 2
+    per = tiles * 4 * 16  # values a launch records
+    stamps = hip.Buffer(records * per * 8)
+    c = hip.Buffer(n * n * 2)
+    out = {}
+    for name in ("bf16", "i8"):
+        if name == "bf16":
+            bufs = [hip.Buffer.of(bf16(rng.standard_normal((n, n), dtype=np.float32) / np.float32(64.0))) for _ in "ab"]
+            stage_k = 32
+
+            def launch(slot, handle, bufs=bufs):
+                e = lib.wave_stamps_bf16(bufs[0].ptr, bufs[1].ptr, c.ptr, stamps.ptr + 8 * per * slot, n, handle)
+                if e != 0:
+                    raise RuntimeError(f"wave_stamps_bf16: hipError {e}")
+        else:
+            bufs = [hip.Buffer.of(rng.integers(-127, 128, (n, n), dtype=np.int8)) for _ in "ab"]
+            bufs += [hip.Buffer.of(rng.uniform(1e-3, 1e-2, n).astype(np.float32)) for _ in "rc"]
+            stage_k = 64
+
+            def launch(slot, handle, bufs=bufs):
+                e = lib.wave_stamps_i8(bufs[0].ptr, bufs[1].ptr, c.ptr, bufs[2].ptr, bufs[3].ptr,
+                                       stamps.ptr + 8 * per * slot, n, handle)  # fmt: skip
+                if e != 0:
+                    raise RuntimeError(f"wave_stamps_i8: hipError {e}")
+        t = timed([0], stream, steps, warmup, launch=launch)
+        for slot in range(records):
+            launch(slot, stream.handle)
+        stream.synchronize()
+        raw = stamps.download((records, tiles, 4, 16), np.uint64).astype(np.int64)
+        launches = []
+        for r in raw:
+            t0 = r[:, :, 0].min()
+            at = (r[:, :, 0:5] - t0) / 100.0  # us: the reference clock counts at 100 MHz
+            loop_us = (r[:, :, 2] - r[:, :, 1]) / 100.0
+            cycles = (r[:, :, 7] - r[:, :, 6]).astype(np.float64)
+            xcd = r[:, 0, 10]
+            spread = lambda v: [round(float(v.min()), 2), round(float(np.median(v)), 2), round(float(v.max()), 2)]
+            launches.append({
+                "t0": int(t0), "end": int(r[:, :, 4].max()),
+                "first_mfma_us": spread(at[:, :, 1]), "loop_done_us": spread(at[:, :, 2]),
+                "stores_issued_us": spread(at[:, :, 3]), "stores_done_us": spread(at[:, :, 4]),
+                "cycles_per_stage": round(float(np.median(cycles)) / (n // stage_k), 1),
+                "clock_mhz": round(float(np.median(cycles / loop_us)), 1),
+                "xcds": {int(x): {"clock_mhz": round(float(np.median((cycles / loop_us)[xcd == x])), 1),
+                                  "loop_done_us": round(float(np.median(at[xcd == x, :, 2])), 2),
+                                  "last_store_us": round(float(at[xcd == x, :, 4].max()), 2)}
+                         for x in sorted(set(xcd.tolist()))},
+            })  # fmt: skip
+        gaps = [(launches[i + 1]["t0"] - launches[i]["end"]) / 100.0 for i in range(records - 1)]
+        mid = sorted(launches, key=lambda v: v["stores_done_us"][2])[records // 2]
+        mid = {k: v for k, v in mid.items() if k not in ("t0", "end")}
+        out[name] = {"event_us": t["event_ms_per_step"] * 1e3, "median_launch": mid,
+                     "gap_us": {"min": min(gaps), "median": float(np.median(gaps)), "max": max(gaps)}}  # fmt: skip
+        log(f"stamps {name}: {out[name]['event_us']:.1f} us a launch; first MFMA {mid['first_mfma_us']}, loop done "
+            f"{mid['loop_done_us']}, stores done {mid['stores_done_us']}, {mid['cycles_per_stage']} cycles a stage at "
+            f"{mid['clock_mhz']} MHz, gap {np.median(gaps):.2f} us")  # fmt: skip
+        for x in bufs:
+            x.close()
+    stamps.close()
+    c.close()
+    return out
+
+
 TRAFFIC = ROOT / "profiles" / "traffic_workloads.md"
 
 
@@ -717,7 +798,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--only", default="all", choices=["square", "skinny", "mlp", "split", "quantize", "all", "calibrate",
-                                                      "counters", "ceiling", "selector"])  # fmt: skip
+                                                      "counters", "ceiling", "selector", "stamps"])  # fmt: skip
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)  # the CPU leg's own process
     ap.add_argument("--family", choices=["wave"], help="run the square GEMMs on this kernel family")
@@ -735,7 +816,8 @@ def main() -> int:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)  # fmt: skip
         return 2
-    child = cpu_child() if args.only not in ("calibrate", "counters", "ceiling", "selector") and not args.no_cpu else None
+    tools = ("calibrate", "counters", "ceiling", "selector", "stamps")
+    child = cpu_child() if args.only not in tools and not args.no_cpu else None
     L.load()
     dev = hip.describe(0)
     log("device", dev)
@@ -752,6 +834,10 @@ def main() -> int:
         return 0
     if args.only == "selector":
         print(json.dumps({"selector": bench_selector(stream), "device": dev}), flush=True)
+        stream.close()
+        return 0
+    if args.only == "stamps":
+        print(json.dumps({"stamps": bench_stamps(stream, args.steps, args.warmup), "device": dev}), flush=True)
         stream.close()
         return 0
     if args.only == "ceiling":

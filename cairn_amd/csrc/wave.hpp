@@ -127,24 +127,43 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
         const int unit = (8 * j + 2 * q + h) ^ (r & 31);
         *reinterpret_cast<u32x2*>(mine + r * 256 + unit * 8) = w;
       };
+      // The rows go out as non-temporal stores: c is written once and not read again by this launch, and streaming it
+      // past L2 leaves less to write back when the launch ends (4096^3: 0.5-1 us of 105 bf16, 0.7 of 63 int8 W8A8,
+      // side by side against plain stores). The block goes out 32 rows at a time: group i's values are converted
+      // (and go through the epilogue's steps) into LDS, then read back and stored, so that the next group's
+      // arithmetic runs while this group's stores drain (a 4096^3 launch's stores take about 4 us, bound by the
+      // write bandwidth of the XCDs; the dequant and GELU work before them was serial).
+      const int cl = lane & 15;
+      char* out = static_cast<char*>(p.c) + (std::int64_t(row0 + wr) * p.ldc + col0 + wc) * 2 + 16 * cl;
+      auto emit = [&](int i) {  // rows 32 i .. 32 i + 31 of the block, 16 bytes a lane, four rows a read
+#pragma unroll
+        for(int s = 8 * i; s < 8 * i + 8; ++s) {
+          const int r = 4 * s + (lane >> 4);
+          u32x4 v = *reinterpret_cast<const u32x4*>(mine + r * 256 + 16 * (cl ^ ((r & 31) >> 1)));
+          if(r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out + std::int64_t(r) * p.ldc * 2));
+        }
+      };
+      static_assert(Sh::WTM == 32 * FM, "a group of 32 rows a block row");
       if(plain) {
 #pragma unroll
-        for(int i = 0; i < FM; ++i)
+        for(int i = 0; i < FM; ++i) {
 #pragma unroll
           for(int j = 0; j < FN; ++j)
 #pragma unroll
             for(int q = 0; q < 4; ++q)
               put(i, j, q, float(acc[i][j][4 * q]), float(acc[i][j][4 * q + 1]), float(acc[i][j][4 * q + 2]),
                   float(acc[i][j][4 * q + 3]));
+          emit(i);
+          fence();
+        }
       } else {
         with_form(p, [&](auto form) {
           using F = decltype(form);
           float rs[FM];
 #pragma unroll
           for(int i = 0; i < FM; ++i) rs[i] = terms[wr + 32 * i + (lane & 31)];
-#pragma unroll
-          for(int j = 0; j < FN; ++j) {
-            float cs[4][4], bs[4][4];
+          auto col_terms = [&](int j, float (&cs)[4][4], float (&bs)[4][4]) {  // the lane's columns of block column j
 #pragma unroll
             for(int q = 0; q < 4; ++q)
 #pragma unroll
@@ -153,29 +172,44 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
                 cs[q][e] = terms[256 + n];
                 bs[q][e] = terms[512 + n];
               }
+          };
+          auto convert = [&](int i, int j, const float (&cs)[4][4], const float (&bs)[4][4]) {
 #pragma unroll
-            for(int i = 0; i < FM; ++i)
+            for(int q = 0; q < 4; ++q) {
+              float v[4];
 #pragma unroll
-              for(int q = 0; q < 4; ++q) {
-                float v[4];
+              for(int e = 0; e < 4; ++e) v[e] = apply<F>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
+              put(i, j, q, v[0], v[1], v[2], v[3]);
+            }
+          };
+          if constexpr(F::scaled) {
+            // With scales (the W8A8 dequant among them): block column by block column, then the stores. Grouped as
+            // above, the terms of every block column held spilled registers (the dequant ran 2% slower, side by side
+            // at 4096^3).
 #pragma unroll
-                for(int e = 0; e < 4; ++e) v[e] = apply<F>(float(acc[i][j][4 * q + e]), rs[i], cs[q][e], bs[q][e]);
-                put(i, j, q, v[0], v[1], v[2], v[3]);
-              }
+            for(int j = 0; j < FN; ++j) {
+              float cs[4][4], bs[4][4];
+              col_terms(j, cs, bs);
+#pragma unroll
+              for(int i = 0; i < FM; ++i) convert(i, j, cs, bs);
+            }
+#pragma unroll
+            for(int i = 0; i < FM; ++i) emit(i);
+          } else {
+            // Bias and an activation, no scales (the MLP forward's bias + GELU, the longest arithmetic of the
+            // epilogue): grouped, every block column's biases held.
+            float cs[FN][4][4], bs[FN][4][4];
+#pragma unroll
+            for(int j = 0; j < FN; ++j) col_terms(j, cs[j], bs[j]);
+#pragma unroll
+            for(int i = 0; i < FM; ++i) {
+#pragma unroll
+              for(int j = 0; j < FN; ++j) convert(i, j, cs[j], bs[j]);
+              emit(i);
+              fence();
+            }
           }
         });
-      }
-      // The rows go out as non-temporal stores: c is written once and not read again by this launch, and streaming it
-      // past L2 leaves less to write back when the launch ends (4096^3: 0.5-1 us of 105 bf16, 0.7 of 63 int8 W8A8,
-      // side by side against plain stores).
-      const int cl = lane & 15;
-      char* out = static_cast<char*>(p.c) + (std::int64_t(row0 + wr) * p.ldc + col0 + wc) * 2 + 16 * cl;
-#pragma unroll
-      for(int s = 0; s < Sh::WTM / 4; ++s) {
-        const int r = 4 * s + (lane >> 4);
-        u32x4 v = *reinterpret_cast<const u32x4*>(mine + r * 256 + 16 * (cl ^ ((r & 31) >> 1)));
-        if(r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out + std::int64_t(r) * p.ldc * 2));
       }
       return;
     }
@@ -235,13 +269,26 @@ __device__ __forceinline__ void store_partial(const Acc (&acc)[FM][FN], void* pa
       }
 }
 
+// Where a tile's time goes: a Clock is told when the tile starts, when its first MFMA is about to issue (the
+// prologue's loads of stage 0 have landed), when the main loop ends, when the epilogue's stores are issued and when
+// they are done (mark<0> .. mark<4>; the last comes after a wait for every store), then handed the parameters and the
+// tile (record). The library's kernels take NoClock, which does nothing and adds no instruction; a clock-stamp build
+// (tests/cpp/wave_stamps.hip) supplies one that reads the shader and reference clocks.
+struct NoClock {
+  template<int POINT> __device__ __forceinline__ void mark() {}
+  __device__ __forceinline__ void record(const Params&, int, int, int, int) {}
+  static constexpr bool on = false;
+};
+
 // One output tile (tm, tn) over the k stages from s0 on: k counts the operands' elements from stage s0 (all of k
 // for a whole tile; a segment's share in the split round). With PART the accumulators go to `part` as a partial
 // tile (store_partial), else through the epilogue into c. lds is the workgroup's ring, terms its epilogue terms.
-template<class Sh, int OP, bool TA, bool TB, bool RAW, bool PART>
+template<class Sh, int OP, bool TA, bool TB, bool RAW, bool PART, class Clock = NoClock>
 __device__ __forceinline__ void wave_tile(const Params& p, char* lds, float* terms, int tm, int tn, int s0, int k,
                                           void* part) {
   static_assert(Sh::WAVES == 4, "one wave a SIMD");
+  Clock clock;
+  clock.template mark<0>();
   using M = Mfma<OP>;
   using Acc = typename M::Acc;
   constexpr bool AK = !TA, BKM = TB;
@@ -374,6 +421,7 @@ __device__ __forceinline__ void wave_tile(const Params& p, char* lds, float* ter
   wait_loads<(S - 2) * LOADS + Sh::LOADS_A>();
   fenced_barrier();
   unrolled<READS>([&](auto x) { read(B0{}, K0{}, K0{}, x); });
+  clock.template mark<1>();
 
   // The loop's buffer resources, walked a stage at a time: b's from stage S - 1 (iteration 0 loads its b), a's from
   // stage S. Each is computed after MFMAs 8 (its bytes) and 9 (the resource) of the k-step before the one that loads
@@ -441,10 +489,17 @@ __device__ __forceinline__ void wave_tile(const Params& p, char* lds, float* ter
   for(; it + S <= steady; it += S)
     unrolled<S>([&](auto u) { iteration(it + decltype(u)::value, u, Steady{}); });
   for(; it < T; ++it) iteration(it, it % S, Tail{});
+  clock.template mark<2>();
   wait_loads<0>();  // the loads past the last stage land before the workgroup's LDS is given back
 
   if constexpr(PART) store_partial<Sh>(acc, part, wr, wc, lane);
   else store_tile<Sh, RAW>(p, acc, lds, terms, mine_terms, wave, row0, col0, wr, wc, lane);
+  if constexpr(Clock::on) {
+    clock.template mark<3>();
+    wait_loads<0>();
+    clock.template mark<4>();
+    clock.record(p, tm, tn, wave, lane);
+  }
 }
 
 // The ring and the epilogue terms (3 KiB: past the staged store's part of the ring where the ring has room, a
