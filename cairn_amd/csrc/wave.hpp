@@ -183,18 +183,19 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
             }
           };
           if constexpr(F::scaled) {
-            // With scales (the W8A8 dequant among them): block column by block column, then the stores. Grouped as
-            // above, the terms of every block column held spilled registers (the dequant ran 2% slower, side by side
-            // at 4096^3).
+            // With scales (the W8A8 dequant among them): grouped as well, each block column's terms read from LDS
+            // again for every group (held for all groups at once, they spilled registers).
 #pragma unroll
-            for(int j = 0; j < FN; ++j) {
-              float cs[4][4], bs[4][4];
-              col_terms(j, cs, bs);
+            for(int i = 0; i < FM; ++i) {
 #pragma unroll
-              for(int i = 0; i < FM; ++i) convert(i, j, cs, bs);
+              for(int j = 0; j < FN; ++j) {
+                float cs[4][4], bs[4][4];
+                col_terms(j, cs, bs);
+                convert(i, j, cs, bs);
+              }
+              emit(i);
+              fence();
             }
-#pragma unroll
-            for(int i = 0; i < FM; ++i) emit(i);
           } else {
             // Bias and an activation, no scales (the MLP forward's bias + GELU, the longest arithmetic of the
             // epilogue): grouped, every block column's biases held.
