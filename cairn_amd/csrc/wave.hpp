@@ -39,6 +39,7 @@
 // wave_<type>.inc; capi.cpp's kernel table reads the same lists through wave_instances.inc.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <utility>
 #include "epilogue.hpp"
 #include "kernels.hpp"
@@ -182,9 +183,10 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
               put(i, j, q, v[0], v[1], v[2], v[3]);
             }
           };
-          if constexpr(F::scaled) {
-            // With scales (the W8A8 dequant among them): grouped as well, each block column's terms read from LDS
-            // again for every group (held for all groups at once, they spilled registers).
+          constexpr bool integer = std::is_integral_v<std::remove_cvref_t<decltype(acc[0][0][0])>>;
+          if constexpr(F::scaled && integer) {
+            // The W8A8 dequant (int8 accumulators, scales): grouped as well, each block column's terms read from
+            // LDS again for every group (held for all groups at once, they spilled registers).
 #pragma unroll
             for(int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -196,6 +198,18 @@ __device__ __forceinline__ void store_tile(const Params& p, const Acc (&acc)[FM]
               emit(i);
               fence();
             }
+          } else if constexpr(F::scaled) {
+            // Scales on float accumulators: block column by block column, then the stores (grouped, this form's
+            // code made the compiler spill accumulators to scratch after the main loop of every launch).
+#pragma unroll
+            for(int j = 0; j < FN; ++j) {
+              float cs[4][4], bs[4][4];
+              col_terms(j, cs, bs);
+#pragma unroll
+              for(int i = 0; i < FM; ++i) convert(i, j, cs, bs);
+            }
+#pragma unroll
+            for(int i = 0; i < FM; ++i) emit(i);
           } else {
             // Bias and an activation, no scales (the MLP forward's bias + GELU, the longest arithmetic of the
             // epilogue): grouped, every block column's biases held.
