@@ -150,13 +150,14 @@ template<int N, class F> __device__ __forceinline__ void unrolled_loads(F&& f) {
   }(std::make_integer_sequence<int, N>{});
 }
 
-template<int S, int KC>
+template<int S, int KC, int ROWS_B = 64>
 __global__ void __launch_bounds__(256) skinny_ring(Params p, int width) {
-  constexpr int ROWS_B = 64, ROWS_A = 16, UNITS = KC / 16, ROWS_PER_LOAD = 1024 / KC;
+  constexpr int ROWS_A = 16, UNITS = KC / 16, ROWS_PER_LOAD = 1024 / KC;
   constexpr int B_BYTES = ROWS_B * KC, STAGE = (ROWS_B + ROWS_A) * KC;
   constexpr int LOADS_B = ROWS_B / ROWS_PER_LOAD / 4, LOADS_A = ROWS_A / ROWS_PER_LOAD / 4;  // a wave's, a stage
   constexpr int LOADS = LOADS_B + LOADS_A;
   static_assert((KC == 256 || KC == 512 || KC == 1024) && LOADS_B % 4 == 0 && LOADS_A <= 4, "loads go out in groups of four");
+  static_assert(ROWS_B % 16 == 0 && ROWS_B <= 64, "a wave multiplies 16 of b's rows");
   __shared__ __attribute__((aligned(1024))) char lds[S * STAGE];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -206,6 +207,7 @@ __global__ void __launch_bounds__(256) skinny_ring(Params p, int width) {
     barrier();                                         // every wave's: stage st is whole, stage st - 1 is free
     issue(st + S - 1);                                 // into stage st - 1's buffer; past k it reads nothing
     const char* stage = lds + (st % S) * STAGE;
+    if(16 * wave >= ROWS_B) continue;  // uniform: a wave past b's rows loads, and multiplies nothing
 #pragma unroll
     for(int s = 0; s < KC / 64; ++s) {  // the stage's k-steps of 32 elements
       const int u = 4 * s + piece;
@@ -488,17 +490,19 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
                        !(p.c_type == CAIRN_TYPE_F32 && p.accumulate);
     return plain ? cairn::gemm::launch_rows<true>(p, s, row_waves) : cairn::gemm::launch_rows<false>(p, s, row_waves);
   }
-  // The ring with three 512-byte stages (120 KiB of LDS, one workgroup a CU), n spread evenly over the CUs, where that
-  // gives 48 or 56 columns a workgroup (n = 10241 .. 14336: one round of at most 256 workgroups), and for m > 4 at 64
-  // columns up to n = 16384. A load brings two rows' 512 contiguous bytes instead of four rows' 256. Side by side over
-  // n = 4096 .. 28672 and m = 2, 4, 8, 16 (k = 4096) against the forms below: at n = 14336 5.0-5.05 TB/s against
-  // 4.70-4.85 (m = 2 .. 16), at n = 11008 4.79-4.90 against 4.44-4.69, at n = 16384 and m >= 8 4.63-4.71 against
-  // 4.45; at 64 columns and m <= 4, below n = 10240 and past 16384 (two 80 KiB workgroups a CU) they were as fast or
-  // faster. Four 512-byte stages, five or more 256-byte ones, and two 1 KiB ones were all slower at n = 14336.
+  // The half-height ring: three 512-byte stages of 32 rows of b (72 KiB of LDS, two workgroups a CU), n dealt to
+  // 512 workgroups, for m >= 2 from n = 8193 to 16384 and for m > 4 from n = 7681. A load brings two rows' 512
+  // contiguous bytes instead of four rows' 256, and each CU keeps two workgroups' stages in flight. Side by side over
+  // n = 8192 .. 16384 and m = 2, 4, 8, 16 (k = 4096, TB/s): n = 14336 5.12-5.19 against 4.83-4.91 for the form
+  // chosen before (three 512-byte stages of 56 rows, one workgroup a CU), n = 12288 4.94-5.06 against 4.72-4.83,
+  // n = 11008 4.77-4.97 against 4.57-4.67, n = 16384 4.64-4.71 against 4.33-4.63; at n = 8192 m = 8, 16 4.15-4.24
+  // against 3.91-4.07, m = 2, 4 1% behind the streaming form. A width rounded up to 8 (448 workgroups at
+  // n = 14336) left CUs with one workgroup: far slower.
   const int even = cairn_skinny_width(p.n);
-  if(p.m >= 2 && ((even >= 48 && even <= 56) || (p.m > 4 && even == 64 && p.n <= 256 * 64))) {
-    hipLaunchKernelGGL((cairn::gemm::skinny_ring<3, 512>), dim3(unsigned((p.n + even - 1) / even)), dim3(256), 0, s,
-                       p, even);
+  const int half = (p.n + 511) / 512;  // columns a workgroup, 512 workgroups
+  if(p.m >= 2 && half <= 32 && (half > 16 || (p.m > 4 && half == 16))) {
+    hipLaunchKernelGGL((cairn::gemm::skinny_ring<3, 512, 32>), dim3(unsigned((p.n + half - 1) / half)), dim3(256), 0,
+                       s, p, half);
     return hipGetLastError();
   }
   if(p.m >= 2 && p.m <= 4 && p.n >= 2048) {  // rows of b a workgroup: n over the 256 CUs, 16 .. 64
@@ -512,13 +516,11 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
     return hipGetLastError();
   }
   if(p.m > 4 && p.n >= 4096) {
-    // The ring with 256-byte stages (80 KiB of LDS, so two workgroups share a CU where there are more than 256).
-    // Columns a workgroup: 32 below n = 8192 (128 .. 224 workgroups); above, n spread evenly over the 256 CUs where
-    // that is 56 or more (the decode shape, n = 14336: 56, all 256 CUs), else 64. Measured side by side on two boxes
-    // at m = 5 .. 16 against the 512-byte ring (64 columns, 160 KiB) and the register form below n = 8192: 9-19%
-    // faster at n = 5120 .. 7168, even at 14336 (4.8 TB/s either way at 56 columns), 2-4% faster at 8192 and 2-15%
-    // from 16384 on, where two workgroups a CU keep every CU streaming. 32 columns where they give 257 .. 511
-    // workgroups (n = 10240 .. 14336) measured far slower.
+    // The ring with 256-byte stages (80 KiB of LDS, so two workgroups share a CU where there are more than 256), below
+    // n = 7681 and above 16384 (between them the half-height ring above). Columns a workgroup: 32 below n = 8192
+    // (128 .. 224 workgroups), 64 above. Measured side by side on two boxes at m = 5 .. 16 against the 512-byte ring
+    // (64 columns, 160 KiB) and the register form: 9-19% faster at n = 5120 .. 7168 and 2-15% from 16384 on, where two
+    // workgroups a CU keep every CU streaming.
     const int width = p.n < 8192 ? 32 : (even >= 56 ? even : 64);
     hipLaunchKernelGGL((cairn::gemm::skinny_ring<4, 256>), dim3(unsigned((p.n + width - 1) / width)), dim3(256), 0, s,
                        p, width);

@@ -419,8 +419,8 @@ def test_skinny_decode_shapes_keep_the_contract(m):
     assert H.outside(v, exact, room) == 0
 
 
-# m >= 2 with n spread over the CUs at 48 or 56 columns (n = 10241 .. 14336), and m > 4 at 64 columns up to n = 16384,
-# take the ring form with 512-byte stages; other m > 4 with n >= 4096 the ring form with 256-byte stages (32 columns a
+# m >= 2 with n = 8193 .. 16384, and m > 4 from n = 7681, take the half-height ring (32 rows of b a workgroup at most,
+# n over 512 workgroups, 512-byte stages); other m > 4 with n >= 4096 the ring form with 256-byte stages (32 columns a
 # workgroup below n = 8192, 64 above, two workgroups a CU past 256 of them), m = 1 with n >= 2048 and k <= 4096 the row-streaming one (whole rows
 # of b a wave, dealt evenly: a wave's share differs from the next one's by at most a row), m = 2 .. 4 with n >= 2048 the streaming MFMA form (16 rows of b a wave; whole groups of 8 steps, then
 # single steps, the last one partial), the rest the register form: tails in each.
@@ -431,7 +431,7 @@ def test_skinny_decode_shapes_keep_the_contract(m):
                                    (8, 4096, 1000), (11, 6150, 264), (6, 20003, 520), (16, 28672, 136),
                                    (5, 4095, 256), (1, 14336, 4096), (1, 12289, 1000), (1, 12288, 520),
                                    (2, 11008, 4104), (4, 10241, 4096), (9, 12289, 24), (16, 16384, 520),
-                                   (5, 14336, 1000)])
+                                   (5, 14336, 1000), (6, 8000, 1000), (3, 8193, 264), (12, 16384, 4096)])
 def test_skinny_tails_keep_the_contract(m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = H.normal_bf16(rng, (m, k), 1.0)
@@ -465,8 +465,8 @@ def test_every_skinny_form_applies_the_epilogue_in_its_stated_order(act):
     sizes), bf16 out: equal, bit for bit, to the stated steps applied in f32 to what the same form computes without
     them: bf16(act((f32(acc) * rs[i]) * cs[j] + bias[j]))."""
     rng = np.random.default_rng(31 + act)
-    # rows, stream, ring (256-byte stages), register, ring (512-byte stages)
-    for m, n, k in [(1, 4100, 1024), (3, 4100, 1000), (6, 8256, 512), (3, 200, 256), (6, 14336, 520)]:
+    # rows, stream, ring (256-byte stages), register, half-height ring (512-byte stages)
+    for m, n, k in [(1, 4100, 1024), (3, 4100, 1000), (6, 6000, 512), (3, 200, 256), (6, 14336, 520)]:
         a = H.normal_bf16(rng, (m, k), 1.0)
         b = H.normal_bf16(rng, (n, k), 1.0)
         rs = rng.uniform(0.25, 2.0, m).astype(np.float32)
