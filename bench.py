@@ -235,8 +235,27 @@ def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
                      "efficiency": round(ch["efficiency"], 4),
                      "median_tflops": flops / (t["median_ms"] * 1e-3) / 1e12,
                      "tflops_whole_rounds": flops / (tw["event_ms_per_step"] * 1e-3) / 1e12, **t}  # fmt: skip
+        # The same GEMM with its partial last round split over the whole machine (split_units = 256), where it has
+        # one: the alternative the selector weighs against running that round whole.
+        forced = L.Desc.from_buffer_copy(d)
+        forced.split_units = 256
+        forced.workspace, forced.workspace_bytes = None, 0
+        fneed = L.workspace(forced)  # 0 where the GEMM has no partial last round to split
+        fws = hip.Buffer(fneed) if fneed else None
+        if fws:
+            forced.workspace, forced.workspace_bytes = fws.ptr, fneed
+        fch = L.select(forced) if fws else {"split_tiles": 0}
+        if fch["split_tiles"]:
+            tf = timed([forced], stream, launches, warmup // 2)
+            out[name]["split_forced"] = {"split_tiles": fch["split_tiles"], "split_units": fch["split_units"],
+                                         "efficiency": round(fch["efficiency"], 4),
+                                         "tflops": flops / (tf["event_ms_per_step"] * 1e-3) / 1e12}  # fmt: skip
+        if fws:
+            fws.close()
+        forced_note = (f"; split over 256 units {out[name]['split_forced']['tflops']:.0f}"
+                       if "split_forced" in out[name] else "")  # fmt: skip
         log(f"mlp {name}: {out[name]['tflops']:.0f} TFLOP/s on {ch['name']} (split {ch['split_tiles']} tiles; "
-            f"whole rounds {out[name]['tflops_whole_rounds']:.0f})")  # fmt: skip
+            f"whole rounds {out[name]['tflops_whole_rounds']:.0f}{forced_note})")  # fmt: skip
     t = timed([fwd, bwd_x, bwd_w], stream, 3 * launches, warmup)
     out["step_ms"] = 3 * t["event_ms_per_step"]
     out["tflops"] = 3 * flops / (out["step_ms"] * 1e-3) / 1e12
