@@ -238,14 +238,15 @@ __global__ void __launch_bounds__(256) skinny_ring(Params p, int width) {
   }
 }
 
-// The row-streaming form, for m = 1 and k <= 4096 (a decode step's one token): a wave owns a contiguous
-// run of b's rows (the output's columns), wave w of `waves` rows [w n / waves, (w + 1) n / waves), so that no two
-// waves' runs differ by more than a row, and reads each row front to back, 1 KiB a load (64 lanes x 16 bytes), so
-// every wave streams one contiguous region of HBM, as a plain copy does. The arithmetic is small enough for the
-// vector ALUs: lane l holds a's 16-byte pieces at the same k as its pieces of b (loaded once), multiplies and adds
-// in f32 (every product of two bf16 exact, each sum one rounding: the contract), and the wave's 64 partial sums of a
-// row meet in a fixed DPP pattern, so two runs give the same bits. The next row's loads are issued before the
-// current row is summed: two rows of a wave in flight, KCH KiB each.
+// The row-streaming form, for m = 1 and 2 and k <= 4096 (a decode step's one or two tokens): a wave owns a
+// contiguous run of b's rows (the output's columns), wave w of `waves` rows [w n / waves, (w + 1) n / waves), so that
+// no two waves' runs differ by more than a row, and reads each row front to back, 1 KiB a load (64 lanes x 16 bytes),
+// so every wave streams one contiguous region of HBM, as a plain copy does. The arithmetic is small enough for the
+// vector ALUs: lane l holds a's 16-byte pieces at the same k as its pieces of b (loaded once), and v_dot2_f32_bf16
+// adds two products of the packed pairs into its f32 sum an instruction (no widening of either operand), and the
+// wave's 64 partial sums of a row meet in a fixed DPP pattern, so two runs give the same bits. The next row's loads
+// are issued before the current row is summed: two rows of a wave in flight, KCH KiB each.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 template<int M, int KCH, bool PLAIN, int OUT>
 __global__ void __launch_bounds__(256, 3) skinny_rows(Params p, int waves) {
   const int t = threadIdx.x, lane = t & 63;
@@ -331,13 +332,14 @@ __global__ void __launch_bounds__(256, 3) skinny_rows(Params p, int waves) {
     for(int c = 0; c < KCH; ++c)
 #pragma unroll
       for(int e = 0; e < 4; ++e) {
+        // Each element goes through a scalar first: this compiler turned a bit_cast of an element of a vector
+        // (xr[c][e]) into a read of element 0 whatever e was.
         const std::uint32_t wb = xr[c][e];
-        const float b0 = __builtin_bit_cast(float, wb << 16), b1 = __builtin_bit_cast(float, wb & 0xffff0000u);
+        const bf16x2 vb = __builtin_bit_cast(bf16x2, wb);
 #pragma unroll
         for(int i = 0; i < M; ++i) {
           const std::uint32_t wa = xa[i][c][e];
-          acc[i] = __builtin_fmaf(__builtin_bit_cast(float, wa << 16), b0, acc[i]);
-          acc[i] = __builtin_fmaf(__builtin_bit_cast(float, wa & 0xffff0000u), b1, acc[i]);
+          acc[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wa), vb, acc[i], false);
         }
       }
     const int n = first + r;
@@ -377,12 +379,14 @@ __global__ void __launch_bounds__(256, 3) skinny_rows(Params p, int waves) {
   if(r < rows) row(r, xb[0], t0);
 }
 
-// The row-streaming form's launch: its instance for the epilogue (PLAIN: no terms, c not read) and output type.
-template<bool PLAIN> hipError_t launch_rows(const Params& p, hipStream_t s, int waves) {
+// The row-streaming form's launch: its instance for m (1 or 2), the epilogue (PLAIN: no terms, c not read) and the
+// output type. `lds` bytes of LDS a workgroup, which the kernel does not touch, cap the workgroups a CU holds at once
+// (0: as many as the registers allow).
+template<int M, bool PLAIN> hipError_t launch_rows(const Params& p, hipStream_t s, int waves, unsigned lds) {
   const dim3 grid(unsigned(waves / 4)), block(256);
-  if(p.c_type == CAIRN_TYPE_BF16) hipLaunchKernelGGL((skinny_rows<1, 8, PLAIN, CAIRN_TYPE_BF16>), grid, block, 0, s, p, waves);
-  else if(p.c_type == CAIRN_TYPE_F16) hipLaunchKernelGGL((skinny_rows<1, 8, PLAIN, CAIRN_TYPE_F16>), grid, block, 0, s, p, waves);
-  else hipLaunchKernelGGL((skinny_rows<1, 8, PLAIN, CAIRN_TYPE_F32>), grid, block, 0, s, p, waves);
+  if(p.c_type == CAIRN_TYPE_BF16) hipLaunchKernelGGL((skinny_rows<M, 8, PLAIN, CAIRN_TYPE_BF16>), grid, block, lds, s, p, waves);
+  else if(p.c_type == CAIRN_TYPE_F16) hipLaunchKernelGGL((skinny_rows<M, 8, PLAIN, CAIRN_TYPE_F16>), grid, block, lds, s, p, waves);
+  else hipLaunchKernelGGL((skinny_rows<M, 8, PLAIN, CAIRN_TYPE_F32>), grid, block, lds, s, p, waves);
   return hipGetLastError();
 }
 
@@ -480,15 +484,28 @@ hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 4096, the LDS ring
   // (4.6 against 4.4 TB/s for the register form at m = 16, and 4.0 for the streaming form, whose loads of a's 16
   // rows double the L2 traffic); otherwise the register form.
-  // Whole rows a wave, dealt evenly: 8192 waves from n = 12288, 4096 from n = 4096, else 2048 (at most 12 of them a CU
-  // at once: 168 registers). Side by side at k = 4096 (TB/s): n = 14336 5.74 for 8192 waves, 5.64 for 4096, 5.50 for
-  // 2048; n = 12288 5.74, 5.62, 5.41; n = 8192 5.74, 5.83, 5.59; n = 4096 even.
-  const int row_waves = p.n >= 12288 ? 8192 : (p.n >= 4096 ? 4096 : 2048);
+  // Whole rows a wave, dealt evenly, on packed bf16 dot products, for m = 1 from n = 2048 and m = 2 from n = 4096.
+  // m = 1: 8192 waves from n = 8192, 4096 from 4096, else 2048, at most four workgroups a CU (72 registers would let
+  // seven share one; the LDS asked for leaves room for four). Side by side at k = 4096 (TB/s) against the form before
+  // (f32 FMAs on operands widened in registers, 165 registers: 12 waves a CU): n = 8192 6.04-6.05 against 5.66-5.68,
+  // 14336 5.76-5.78 against 5.49-5.54, 16384 5.72-5.75 against 5.55-5.66, 28672 5.89-5.90 against 5.88-5.91; without
+  // the cap 5.62, 5.69 and 5.74 at 14336, 16384 and 28672, with three workgroups a CU 5.68, 5.75, 5.92.
+  // m = 2 (134 registers: three workgroups a CU): 8192 waves from n = 16384, 4096 from 8192, else 2048; against the
+  // forms it replaced (the half-height ring from 8193, the streaming form below): n = 4096 4.44 against 3.21, 8192
+  // 5.46 against 5.06-5.13, 11008 5.03-5.05 against 4.85-5.01, 14336 5.37-5.38 against 5.25-5.28, 16384 5.45 against
+  // 4.74, 28672 5.87 against 5.07. m = 4 in this form (198 registers) ran 4.86 against the ring's 5.17-5.19.
+  const int row_waves = p.m == 1 ? (p.n >= 8192 ? 8192 : (p.n >= 4096 ? 4096 : 2048))
+                                 : (p.n >= 16384 ? 8192 : (p.n >= 8192 ? 4096 : 2048));
   const int most = (p.n + row_waves - 1) / row_waves;  // rows the busiest wave streams
-  if(p.m == 1 && p.k <= 4096 && p.n >= 2048 && std::int64_t(most + 1) * p.ldb * 2 < 0x7f000000LL) {
+  if(((p.m == 1 && p.n >= 2048) || (p.m == 2 && p.n >= 4096)) && p.k <= 4096 &&
+     std::int64_t(most + 1) * p.ldb * 2 < 0x7f000000LL) {
     const bool plain = !p.row_scale && !p.col_scale && !p.bias && p.act == CAIRN_ACT_NONE &&
                        !(p.c_type == CAIRN_TYPE_F32 && p.accumulate);
-    return plain ? cairn::gemm::launch_rows<true>(p, s, row_waves) : cairn::gemm::launch_rows<false>(p, s, row_waves);
+    constexpr unsigned FOUR = 160u * 1024 / 5 + 64;  // of the CU's 160 KiB of LDS: room for four workgroups, not five
+    if(p.m == 1)
+      return plain ? cairn::gemm::launch_rows<1, true>(p, s, row_waves, FOUR)
+                   : cairn::gemm::launch_rows<1, false>(p, s, row_waves, FOUR);
+    return plain ? cairn::gemm::launch_rows<2, true>(p, s, row_waves, 0) : cairn::gemm::launch_rows<2, false>(p, s, row_waves, 0);
   }
   // The half-height ring: three 512-byte stages of 32 rows of b (72 KiB of LDS, two workgroups a CU), n dealt to
   // 512 workgroups, for m >= 2 from n = 8193 to 16384 and for m > 4 from n = 7681. A load brings two rows' 512

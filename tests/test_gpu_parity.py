@@ -431,7 +431,8 @@ def test_skinny_decode_shapes_keep_the_contract(m):
                                    (8, 4096, 1000), (11, 6150, 264), (6, 20003, 520), (16, 28672, 136),
                                    (5, 4095, 256), (1, 14336, 4096), (1, 12289, 1000), (1, 12288, 520),
                                    (2, 11008, 4104), (4, 10241, 4096), (9, 12289, 24), (16, 16384, 520),
-                                   (5, 14336, 1000), (6, 8000, 1000), (3, 8193, 264), (12, 16384, 4096)])
+                                   (5, 14336, 1000), (6, 8000, 1000), (3, 8193, 264), (12, 16384, 4096),
+                                   (2, 14336, 4096), (2, 4100, 1000), (2, 16384, 264), (2, 8192, 4096)])
 def test_skinny_tails_keep_the_contract(m, n, k):
     rng = np.random.default_rng(m * n + k)
     a = H.normal_bf16(rng, (m, k), 1.0)
@@ -443,18 +444,18 @@ def test_skinny_tails_keep_the_contract(m, n, k):
     assert H.outside(got, c0 + exact, H.bound(k, c0, mag)) == 0
 
 
-@pytest.mark.parametrize("n", [2048, 4100, 12289, 14336])
-def test_the_row_streaming_form_rounds_its_own_f32_result_to_each_output_type(n):
-    """m = 1 (the row-streaming form, an instance per output type): bf16 and f16 outputs without an epilogue are, bit
-    for bit, the same form's f32 result rounded to nearest even."""
-    rng = np.random.default_rng(n)
+@pytest.mark.parametrize("m,n", [(1, 2048), (1, 4100), (1, 12289), (1, 14336), (2, 4100), (2, 14336)])
+def test_the_row_streaming_form_rounds_its_own_f32_result_to_each_output_type(m, n):
+    """m = 1 and 2 (the row-streaming form, an instance per output type): bf16 and f16 outputs without an epilogue
+    are, bit for bit, the same form's f32 result rounded to nearest even."""
+    rng = np.random.default_rng(n + m)
     k = 1000
-    a = H.normal_bf16(rng, (1, k), 1.0)
+    a = H.normal_bf16(rng, (m, k), 1.0)
     b = H.normal_bf16(rng, (n, k), 1.0)
-    raw, ch = run_gemm(L.BF16, L.F32, 1, n, k, a, b, trans_b=True)
+    raw, ch = run_gemm(L.BF16, L.F32, m, n, k, a, b, trans_b=True)
     assert ch["family"] == "skinny"
-    got_bf16, _ = run_gemm(L.BF16, L.BF16, 1, n, k, a, b, trans_b=True)
-    got_f16, _ = run_gemm(L.BF16, L.F16, 1, n, k, a, b, trans_b=True)
+    got_bf16, _ = run_gemm(L.BF16, L.BF16, m, n, k, a, b, trans_b=True)
+    got_f16, _ = run_gemm(L.BF16, L.F16, m, n, k, a, b, trans_b=True)
     assert np.array_equal(got_bf16, H.bf16_from_f32(raw))
     assert np.array_equal(got_f16, H.narrow_array(H.F16, raw))
 
@@ -465,8 +466,8 @@ def test_every_skinny_form_applies_the_epilogue_in_its_stated_order(act):
     sizes), bf16 out: equal, bit for bit, to the stated steps applied in f32 to what the same form computes without
     them: bf16(act((f32(acc) * rs[i]) * cs[j] + bias[j]))."""
     rng = np.random.default_rng(31 + act)
-    # rows, stream, ring (256-byte stages), register, half-height ring (512-byte stages)
-    for m, n, k in [(1, 4100, 1024), (3, 4100, 1000), (6, 6000, 512), (3, 200, 256), (6, 14336, 520)]:
+    # rows (m = 1, 2), stream, ring (256-byte stages), register, half-height ring (512-byte stages)
+    for m, n, k in [(1, 4100, 1024), (2, 8192, 1000), (3, 4100, 1000), (6, 6000, 512), (3, 200, 256), (6, 14336, 520)]:
         a = H.normal_bf16(rng, (m, k), 1.0)
         b = H.normal_bf16(rng, (n, k), 1.0)
         rs = rng.uniform(0.25, 2.0, m).astype(np.float32)
