@@ -479,11 +479,11 @@ int cairn_skinny_width(int n) {
 
 hipError_t cairn_skinny(const cairn::gemm::Params& p, hipStream_t s, int) {
   // Four forms, chosen by what measured fastest on the decode shape (n = 14336, k = 4096) in one run of each set:
-  // m = 1, whole rows a wave (5.2 TB/s, against 5.1 for the register form and 4.6 for the ring); m = 2 .. 4, the
-  // streaming form (side by side in one process: m = 4 4.76 against 4.58 TB/s for the register form, m = 3 4.85
-  // against 4.74, m = 2 even; holding a in LDS instead was slower at every m); m = 5 .. 16 and n >= 4096, the LDS ring
-  // (4.6 against 4.4 TB/s for the register form at m = 16, and 4.0 for the streaming form, whose loads of a's 16
-  // rows double the L2 traffic); otherwise the register form.
+  // The forms by m, each chosen side by side in one process: m = 1 and 2, whole rows a wave (below); m = 3 .. 16 from
+  // n = 8193 to 16384, the half-height ring; m = 3, 4 elsewhere from n = 2048, the streaming form (m = 4 4.76 against
+  // 4.58 TB/s for the register form, m = 3 4.85 against 4.74; holding a in LDS instead was slower at every m); m = 5 ..
+  // 16 from n = 4096, the 256-byte ring (4.6 against 4.4 TB/s for the register form at m = 16, and 4.0 for the
+  // streaming form, whose loads of a's 16 rows double the L2 traffic); otherwise the register form.
   // Whole rows a wave, dealt evenly, on packed bf16 dot products, for m = 1 from n = 2048 and m = 2 from n = 4096.
   // m = 1: 8192 waves from n = 8192, 4096 from 4096, else 2048, at most four workgroups a CU (72 registers would let
   // seven share one; the LDS asked for leaves room for four). Side by side at k = 4096 (TB/s) against the form before
