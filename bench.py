@@ -105,13 +105,27 @@ def square(ab: int, out: int, n: int, rng, **kw) -> tuple[L.Desc, list]:
     return d, bufs
 
 
-def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict, dict]:
-    """bf16 and int8 4096^3 on the selector's kernels, or on the 256 x 256 NN kernel of `family` when named."""
+def prepare_square() -> dict:
+    """The square legs' operands, on the device: bf16, int8 with its dequant scales, and fp8 (OCP E4M3) patterns."""
     rng = np.random.default_rng(20261201)
+    n = 4096
+    data = {"bf16": square(L.BF16, L.BF16, n, rng), "i8": square(L.I8, L.BF16, n, rng, row_scale=True)}
+    # fp8 (OCP E4M3) operands, bf16 out, random finite patterns of the format.
+    pats = rng.integers(0, 256, (2, n, n), dtype=np.uint8)
+    pats[(pats & 0x7F) == 0x7F] ^= 0x01  # no NaN patterns (0x7F, 0xFF)
+    bufs = [hip.Buffer.of(pats[0]), hip.Buffer.of(pats[1]), hip.Buffer(n * n * 2)]
+    data["f8"] = (L.desc(L.F8E4M3, L.BF16, n, n, n, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr), bufs)
+    return data
+
+
+def bench_square(stream, steps, warmup, family: str | None = None, data: dict | None = None) -> tuple[dict, dict]:
+    """bf16 and int8 4096^3 on the selector's kernels, or on the 256 x 256 NN kernel of `family` when named; the
+    operands from prepare_square (made here unless given)."""
+    data = data or prepare_square()
     n = 4096
     flops = 2.0 * n**3
     named = (lambda t: L.kernel_named(f"cairn_{family}_{t}_nn_256x256")) if family else (lambda t: 0)
-    d, bufs = square(L.BF16, L.BF16, n, rng)
+    d, bufs = data["bf16"]
     d.kernel = named("bf16")
     choice = L.select(d)
     log("bf16 4096^3 on", choice["name"])
@@ -119,9 +133,7 @@ def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict
     bf = {"kernel": choice["name"], "tflops": flops / (t["wall_ms_per_step"] * 1e-3) / 1e12,
           "kernel_tflops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
           "median_tflops": flops / (t["median_ms"] * 1e-3) / 1e12, **t}  # fmt: skip
-    for x in bufs:
-        x.close()
-    d, bufs = square(L.I8, L.BF16, n, rng, row_scale=True)
+    d, bufs = data["i8"]
     d.kernel = named("i8")
     choice = L.select(d)
     log("int8 4096^3 on", choice["name"])
@@ -130,14 +142,9 @@ def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict
           "kernel_tops": flops / (t["event_ms_per_step"] * 1e-3) / 1e12,
           "median_tops": flops / (t["median_ms"] * 1e-3) / 1e12, **t}  # fmt: skip
     i8["frac"] = i8["kernel_tops"] / PEAK_I8
-    for x in bufs:
-        x.close()
-    # fp8 (OCP E4M3) operands, bf16 out, random finite patterns of the format: the selector's path (widened to f16 on
-    # the way into LDS, the f16 matrix core), and the ring's kernel on the fp8 matrix core, which runs where named.
-    pats = rng.integers(0, 256, (2, n, n), dtype=np.uint8)
-    pats[(pats & 0x7F) == 0x7F] ^= 0x01  # no NaN patterns (0x7F, 0xFF)
-    bufs = [hip.Buffer.of(pats[0]), hip.Buffer.of(pats[1]), hip.Buffer(n * n * 2)]
-    d = L.desc(L.F8E4M3, L.BF16, n, n, n, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr)
+    # fp8: the selector's path (widened to f16 on the way into LDS, the f16 matrix core), and the ring's kernel on the
+    # fp8 matrix core, which runs where named.
+    d, bufs = data["f8"]
     f8 = {}
     for leg, kernel in (("default", named("f8e4m3")), ("matrix_core", L.kernel_named("cairn_wave_f8e4m3_nn_256x256"))):
         d.kernel = kernel
@@ -151,8 +158,9 @@ def bench_square(stream, steps, warmup, family: str | None = None) -> tuple[dict
         r["peak"] = PEAK_BF16 if choice["family"] == "mfma" else PEAK_FP8
         r["frac"] = r["kernel_tflops"] / r["peak"]
         f8[leg] = r
-    for x in bufs:
-        x.close()
+    for _, bufs in data.values():
+        for x in bufs:
+            x.close()
     return bf, i8, f8
 
 
@@ -202,14 +210,22 @@ def bench_quantize(stream, steps, warmup) -> dict:
             "gbps": gbps, "frac": gbps / PEAK_HBM, "median_gbps": moved / (t["median_ms"] * 1e-3) / 1e9, **t}  # fmt: skip
 
 
-def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
+def prepare_mlp() -> dict:
+    """The MLP layer's operands on the device: X, W, bias and dY, and room for Y, dX and dW."""
     rng = np.random.default_rng(3)
     M, K, N = 8192, 4096, 11008
-    x = hip.Buffer.of(bf16(rng.normal(0, 0.02, (M, K)).astype(np.float32)))
-    w = hip.Buffer.of(bf16(rng.normal(0, 0.02, (K, N)).astype(np.float32)))
-    bias = hip.Buffer.of(bf16(rng.normal(0, 0.02, (N,)).astype(np.float32)))
-    dy = hip.Buffer.of(bf16(rng.standard_normal((M, N), dtype=np.float32)))
-    y, dx, dw = hip.Buffer(M * N * 2), hip.Buffer(M * K * 2), hip.Buffer(K * N * 2)
+    return {"x": hip.Buffer.of(bf16(rng.normal(0, 0.02, (M, K)).astype(np.float32))),
+            "w": hip.Buffer.of(bf16(rng.normal(0, 0.02, (K, N)).astype(np.float32))),
+            "bias": hip.Buffer.of(bf16(rng.normal(0, 0.02, (N,)).astype(np.float32))),
+            "dy": hip.Buffer.of(bf16(rng.standard_normal((M, N), dtype=np.float32))),
+            "y": hip.Buffer(M * N * 2), "dx": hip.Buffer(M * K * 2), "dw": hip.Buffer(K * N * 2)}  # fmt: skip
+
+
+def bench_mlp(stream, steps, warmup, family: str | None = None, data: dict | None = None) -> dict:
+    """C3's three GEMMs on operands from prepare_mlp (made here unless given)."""
+    data = data or prepare_mlp()
+    M, K, N = 8192, 4096, 11008
+    x, w, bias, dy, y, dx, dw = (data[k] for k in ("x", "w", "bias", "dy", "y", "dx", "dw"))
     fwd = L.desc(L.BF16, L.BF16, M, N, K, x.ptr, w.ptr, y.ptr, bias=bias.ptr, bias_type=L.BF16, act=L.ACT_GELU)
     bwd_x = L.desc(L.BF16, L.BF16, M, K, N, dy.ptr, w.ptr, dx.ptr, trans_b=True)  # dX = dY W^T (NT)
     bwd_w = L.desc(L.BF16, L.BF16, K, N, M, x.ptr, dy.ptr, dw.ptr, trans_a=True)  # dW = X^T dY (TN)
@@ -264,14 +280,18 @@ def bench_mlp(stream, steps, warmup, family: str | None = None) -> dict:
     return out
 
 
-def bench_split(stream, steps, warmup) -> dict:
-    """The split last round where the selector takes it: 2048 x 8448 x 8192 bf16 (264 tiles: one round, then one tile
-    an XCD over 256 stages), with the workspace it asks for and with none."""
+def prepare_split() -> tuple:
+    """The split leg's operands on the device (a, b) and its output (c)."""
     rng = np.random.default_rng(11)
     m, n, k = 2048, 8448, 8192
-    a = hip.Buffer.of(operands(L.BF16, (m, k), rng))
-    b = hip.Buffer.of(operands(L.BF16, (k, n), rng))
-    c = hip.Buffer(m * n * 2)
+    return hip.Buffer.of(operands(L.BF16, (m, k), rng)), hip.Buffer.of(operands(L.BF16, (k, n), rng)), hip.Buffer(m * n * 2)
+
+
+def bench_split(stream, steps, warmup, data: tuple | None = None) -> dict:
+    """The split last round where the selector takes it: 2048 x 8448 x 8192 bf16 (264 tiles: one round, then one tile
+    an XCD over 256 stages), with the workspace it asks for and with none."""
+    m, n, k = 2048, 8448, 8192
+    a, b, c = data or prepare_split()
     d = L.desc(L.BF16, L.BF16, m, n, k, a.ptr, b.ptr, c.ptr)
     need = L.workspace(d)
     ws = hip.Buffer(max(need, 256))
@@ -868,8 +888,25 @@ def main() -> int:
               "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded normal)",
               "config": {"workload": "bf16 GEMM 4096x4096x4096 NN, fp32 accumulate, bf16 out (BASELINE configs[1])",
                          "m": 4096, "n": 4096, "k": 4096, "layout": "NN", "parallelism": "none (1 GPU)"}}  # fmt: skip
+    # The legs run from the least to the most clock-sensitive: the HBM-bound decode and quantize legs first, the
+    # compute-bound split and MLP legs next, the square GEMMs (the headline) last, and the compute legs' operands are
+    # made and uploaded before any leg, so that those legs follow each other with no host work between them. After
+    # even a tenth of a second idle (the host generating operands) the GPU's clock takes some milliseconds of work to
+    # come back: a burst of 20 launches of C2 right after ran 1096-1192 TFLOP/s against 1270-1283 once back. Each leg
+    # still does exactly its `warmup` untimed launches and `steps` timed ones.
+    ready = {}
+    if args.only == "all":
+        ready = {"split": prepare_split(), "mlp": prepare_mlp(), "square": prepare_square()}
+    if args.only in ("skinny", "all"):
+        record["skinny"] = bench_skinny(stream, args.steps, args.warmup)
+    if args.only in ("quantize", "all"):
+        record["quantize"] = bench_quantize(stream, args.steps, args.warmup)
+    if args.only in ("split", "all"):
+        record["split"] = bench_split(stream, args.steps, args.warmup, ready.get("split"))
+    if args.only in ("mlp", "all"):
+        record["mlp"] = bench_mlp(stream, args.steps, args.warmup, args.family, ready.get("mlp"))
     if args.only in ("square", "all"):
-        bf, i8, f8 = bench_square(stream, args.steps, args.warmup, args.family)
+        bf, i8, f8 = bench_square(stream, args.steps, args.warmup, args.family, ready.get("square"))
         record["value"] = bf["tflops"]
         record["ms_per_step"] = bf["wall_ms_per_step"]
         traffic = measured_traffic(bf["kernel"])
@@ -889,14 +926,6 @@ def main() -> int:
                                                "within the contract at long k only)", **f8["matrix_core"]}  # fmt: skip
         log(f"bf16 {bf['tflops']:.0f} TFLOP/s ({bf['kernel_tflops'] / PEAK_BF16:.1%}); int8 {i8['tops']:.0f} TOPS; "
             f"f8e4m3 {f8['default']['tflops']:.0f} TFLOP/s, {f8['matrix_core']['tflops']:.0f} on the fp8 core")
-    if args.only in ("skinny", "all"):
-        record["skinny"] = bench_skinny(stream, args.steps, args.warmup)
-    if args.only in ("mlp", "all"):
-        record["mlp"] = bench_mlp(stream, args.steps, args.warmup, args.family)
-    if args.only in ("split", "all"):
-        record["split"] = bench_split(stream, args.steps, args.warmup)
-    if args.only in ("quantize", "all"):
-        record["quantize"] = bench_quantize(stream, args.steps, args.warmup)
     record["device"] = dev
     if child is not None:
         record["cpu_baseline"] = cpu_result(child)
