@@ -6,9 +6,11 @@ bf16 output) with int8 TOPS (W8A8, fused dequant to bf16), as a fraction of the 
 A step is one 4096^3 bf16 GEMM on inputs already resident in HBM. W untimed steps, then exactly K timed steps between
 two synchronizations; `value` is 2 * 4096^3 * K / wall seconds. The default W (400, about 45 ms of the 4096^3 GEMM)
 outlasts the clock ramp of a GPU coming out of idle: after half a second idle, the first 50 launches of the 4096^3
-GEMM average 255 us, launches 100-149 113 us, and from about launch 300 on it holds 109 us. The same run also measures, as extra records:
-int8 W8A8 4096^3 TOPS; f8e4m3 4096^3 widened (the selector's path) and on the fp8 matrix core; the skinny decode GEMMs (m = 1, 4, 16; n = 14336; k = 4096; b stored n x k) in HBM GB/s,
-rotating enough copies of b that the 256 MB MALL cannot hold them; the MLP forward + backward (3 GEMMs); the
+GEMM average 255 us, launches 100-149 113 us, and from about launch 300 on it holds 109 us. With a short W the legs'
+order and the operands made before any leg keep the GPU busy from one compute leg to the next (main). The same run
+also measures, as extra records: int8 W8A8 4096^3 TOPS; f8e4m3 4096^3 widened (the selector's path) and on the fp8
+matrix core; the skinny decode GEMMs (m = 1, 4, 16; n = 14336; k = 4096; b stored n x k) in HBM GB/s, rotating
+enough copies of b that the 256 MB MALL cannot hold them; the MLP forward + backward (3 GEMMs); the split round; the
 bf16 -> int8 activation quantize in HBM GB/s; and the reference's CPU loop timed on this host (cpu_baseline).
 
 `roofline` is for the dominant kernel (the 4096^3 bf16 GEMM): achieved = 2 * 4096^3 FLOP / its average launch
